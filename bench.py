@@ -1,0 +1,203 @@
+"""Headline benchmark: paged decode step on one MI355X.
+
+Workload (BASELINE.json metric "paged-attn decode GB/s (% HBM peak) + tokens/sec
+at B=32, 8k ctx, 32q/8kv hd128"): Mistral-Small-22B-shaped decode step, B=32
+sequences all at 8192 tokens of context, 32 query heads / 8 kv heads,
+head_dim 128, fp16, block_size 16, physical blocks shuffled across a pool sized
+for 300k tokens.  One step = the fused KV write of each sequence's new token
+plus paged GQA attention over the whole context (split-K + in-launch LSE
+merge): a single kernel launch, inputs resident in HBM.
+
+value       algorithmic bytes of the step / wall time per step (GB/s)
+roofline    the decode kernel's algorithmic bytes / its average duration from
+            HIP events on the launch stream, against 8 TB/s
+cpu_baseline the reference's CPU torch path (per-sequence gather +
+            repeat_interleave + SDPA, oracle/ref_torch.py) on the same inputs
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "vllm-apple_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged-attn decode GB/s (% HBM peak) + tokens/sec at B=32, 8k ctx, 32q/8kv hd128"
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--partition", type=int, default=0, help="split-K tokens (0 = auto)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="approximate budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def traffic_from_profile() -> float | None:
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    f = REPO / "profiles" / "paged_decode_c2_8k_traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            try:
+                return float(line.split("=", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(batch, budget_s: float) -> dict:
+    """Time the reference CPU torch path on a bounded sample of the same step."""
+    import torch
+
+    from oracle import ref_torch
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    # Sample: the first n sequences of the step, copied to host in the vLLM layout
+    # the reference torch path reads (conversion not timed).
+    n = min(4, batch.num_seqs)
+    bt = batch.block_table[:n].cpu()
+    nblk = (batch.extra["seq_lens_host"][0] + 15) // 16
+    used = bt[:, :nblk].reshape(-1).long()
+    kc = ref_torch.kernel_to_vllm_layout(batch.k_cache[used].cpu())
+    vc = ref_torch.kernel_to_vllm_layout(batch.v_cache[used].cpu())
+    local_bt = torch.arange(used.numel(), dtype=torch.int32).view(n, nblk)
+    q = batch.query[:n].cpu()
+    lens = batch.extra["seq_lens_host"][:n]
+    kv = batch.num_kv_heads
+    ref_torch.decode_sdpa(q, kc, vc, local_bt, lens, batch.scale, kv)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        ref_torch.decode_sdpa(q, kc, vc, local_bt, lens, batch.scale, kv)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    D, H = batch.head_size, batch.num_q_heads
+    sample_bytes = sum(lens) * kv * D * 2 * 2 + 2 * n * H * D * 2
+    return {
+        "value": round(sample_bytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n} of {batch.num_seqs} sequences (ctx {lens[0]}) of the same decode step, "
+                   f"reference torch path (mps_attn.py:284-357) on host, fp16 storage, "
+                   f"median of {len(times)} runs = {med * 1e3:.1f} ms "
+                   f"({n / med:.1f} tok/s); {torch.__version__}"),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+        return 2
+    import torch
+
+    from vllm_apple_amd import _lib, kernels, workloads
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b = workloads.c2_decode(device=dev, fixed_len=args.ctx, batch=args.batch)
+    out = torch.empty_like(b.query)
+    max_len = b.max_seq_len
+
+    def step():
+        kernels.paged_decode(b.query, b.k_cache, b.v_cache, b.block_table, b.seq_lens,
+                             scale=b.scale, max_seq_len=max_len, output=out,
+                             new_keys=b.new_k, new_values=b.new_v,
+                             partition_size=args.partition)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: K steps, synchronize on both sides (one rank: no barrier).
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record(stream)
+        step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+    kern_avg_ms = sum(kern_ms) / len(kern_ms)
+    ms_per_step = wall * 1e3 / args.steps
+
+    alg_bytes = b.decode_algorithmic_bytes()
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = alg_bytes / (kern_avg_ms * 1e-3) / 1e9
+    traffic = traffic_from_profile()
+    _, part = kernels.decode_workspace_size(kernels.make_params(
+        key_cache=b.k_cache, value_cache=b.v_cache, layout="kernel",
+        num_query_heads=b.num_q_heads, scale=b.scale, num_seqs=b.num_seqs,
+        max_seq_len=max_len, max_blocks_per_seq=b.block_table.shape[1],
+        partition_size=args.partition))
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic N(0,1) q/k/v and cache, seeded (workloads.c2_decode seed 1002)",
+        "config": {
+            "workload": "C2-headline: Mistral-Small-22B-shaped fused KV write + paged decode, "
+                        "all ctx=8192",
+            "batch": args.batch, "ctx": args.ctx, "num_q_heads": b.num_q_heads,
+            "num_kv_heads": b.num_kv_heads, "head_dim": b.head_size, "block_size": 16,
+            "pool_blocks": int(b.k_cache.shape[0]), "split_k_partition": part,
+            "algorithmic_bytes_per_step": alg_bytes,
+        },
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(args.batch / (ms_per_step * 1e-3), 1),
+        "kernel_ms": {"avg": round(kern_avg_ms, 5), "min": round(kern_ms[0], 5),
+                      "p50": round(kern_ms[len(kern_ms) // 2], 5),
+                      "p90": round(kern_ms[int(len(kern_ms) * 0.9)], 5)},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_kernel<128>",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "device": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(b, args.cpu_seconds)
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,281 @@
+/*
+ * vllm_apple_amd.h -- C ABI of the MI355X (gfx950) paged-attention hot path.
+ *
+ * Every entry point takes device pointers owned by the caller, explicit
+ * element strides and a HIP stream (passed as void*), enqueues its kernels on
+ * that stream and returns without synchronising.  The return value is a
+ * status code (VAA_OK == 0, negative on error); vaa_last_error() returns a
+ * thread-local message for the last failure on the calling thread.
+ *
+ * Data types: K/V cache, queries, outputs and activations are IEEE fp16
+ * (uint16_t storage).  Block tables, sequence lengths, token->sequence maps
+ * and positions are int32.  Slot mappings may be int32 (engine) or int64
+ * (vLLM metadata), selected by an argument.
+ *
+ * Cache layouts are described by (stride_block, stride_head, stride_token)
+ * in elements, so both layouts used by the reference are first-class:
+ *   kernel/engine layout  K,V each [num_blocks, num_kv_heads, block_size, D]
+ *       (vllm_apple/metal/kv_cache.py:213-219, engine/kv_cache.py:142-148)
+ *   vLLM-facing layout    kv_cache[2, num_blocks, block_size, num_kv_heads, D]
+ *       (vllm_apple/v1/attention/backends/metal_attn.py:171-185)
+ * The innermost (head_size) dimension must be contiguous.
+ *
+ * Device-side guards: every kernel skips (never dereferences) a block id
+ * outside [0, num_blocks) and a slot outside [0, num_blocks*block_size), so a
+ * bad index cannot fault the GPU.  Range validation that raises errors is
+ * done on the host by the Python layer, as the reference does
+ * (vllm_apple/engine/kv_cache.py:300-420).
+ */
+#ifndef VLLM_APPLE_AMD_H_
+#define VLLM_APPLE_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VAA_ABI_VERSION 1
+
+enum {
+  VAA_OK = 0,
+  VAA_ERR_INVALID_ARG = -1,  /* bad shape, stride, alignment or null pointer */
+  VAA_ERR_UNSUPPORTED = -2,  /* head size / block size / group size not built */
+  VAA_ERR_HIP = -3,          /* HIP runtime error (launch or device query)    */
+  VAA_ERR_WORKSPACE = -4     /* split-K workspace missing or too small        */
+};
+
+/* Index element types for slot mappings. */
+enum { VAA_INDEX_I32 = 0, VAA_INDEX_I64 = 1 };
+
+/*
+ * Attention parameters.  Mirrors FusedAttentionParams / PagedAttentionParams
+ * (vllm_apple/metal/kernels/paged_attention_fused.metal:24-49,
+ *  vllm_apple/engine/ops/attention.py:51-157) with 64-bit strides, plus the
+ * cache capacity (device-side guard) and the split-K partition size.
+ */
+typedef struct vaa_attn_params {
+  float scale;                /* softmax scale, usually 1/sqrt(head_size)     */
+  int32_t num_seqs;           /* rows of block_table / seq_lens               */
+  int32_t max_seq_len;        /* upper bound of seq_lens (sizes the grid)     */
+  int32_t max_blocks_per_seq; /* block_table row stride in elements           */
+  int32_t head_size;          /* 32, 64, 96 or 128                            */
+  int32_t block_size;         /* tokens per cache block, multiple of 16       */
+  int32_t num_kv_heads;
+  int32_t num_query_heads;
+  int32_t queries_per_kv;     /* num_query_heads / num_kv_heads, <= 16        */
+  int32_t partition_size;     /* split-K tokens per partition; 0 = automatic  */
+  int64_t num_blocks;         /* cache capacity in blocks                     */
+  int64_t k_stride_block, k_stride_head, k_stride_token;
+  int64_t v_stride_block, v_stride_head, v_stride_token;
+  int64_t q_stride_token, q_stride_head;
+  int64_t o_stride_token, o_stride_head;
+  int64_t new_kv_stride_token, new_kv_stride_head; /* new K and new V        */
+} vaa_attn_params;
+
+/* Thread-local message describing the last error on this thread. */
+const char* vaa_last_error(void);
+int vaa_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * KV cache writes (bit-exact copies)
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Replaces metal_write_kv_batch (vllm_apple/metal/native/kv_write.c:33-78),
+ * bound by ctypes at vllm_apple/metal/bridge/metal_paged_attention_v2.py:574-607.
+ * Same arguments, now device pointers, plus num_blocks (guard) and a stream.
+ * Source K/V are contiguous [num_tokens, num_kv_heads, head_size]; for each
+ * token t and head h the head_size elements go to
+ * block_ids[t]*stride_block + h*stride_head + token_offsets[t]*stride_token.
+ * Tokens whose block id is outside [0, num_blocks) or whose offset is
+ * negative are skipped.
+ */
+int vaa_write_kv_batch(uint16_t* key_dst, uint16_t* value_dst,
+                       const uint16_t* key_src, const uint16_t* value_src,
+                       const int64_t* block_ids, const int64_t* token_offsets,
+                       int num_tokens, int num_kv_heads, int head_size,
+                       int64_t stride_block, int64_t stride_head,
+                       int64_t stride_token, int64_t num_blocks, void* stream);
+
+/*
+ * Replaces metal_write_kv_single (vllm_apple/metal/native/kv_write.c:84-107):
+ * one token, block id and offset passed by value.
+ */
+int vaa_write_kv_single(uint16_t* key_dst, uint16_t* value_dst,
+                        const uint16_t* key_src, const uint16_t* value_src,
+                        int64_t block_id, int64_t token_offset,
+                        int num_kv_heads, int head_size, int64_t stride_block,
+                        int64_t stride_head, int64_t stride_token,
+                        int64_t num_blocks, void* stream);
+
+/*
+ * Replaces the kv_write_prefill kernel (vllm_apple/engine/ops/kv_write.py:118-156,
+ * host KVWriteOp.encode_prefill :336-402) and the torch scatter path
+ * (vllm_apple/v1/attention/backends/base_attn.py:308-342): for token t with
+ * s = slot_mapping[t] >= 0, K[s/bs, h, s%bs, :] = new_keys[t, h, :] and the
+ * same for V.  Negative slots (padding) and slots >= num_blocks*block_size
+ * are skipped.  Uses p->num_kv_heads, head_size, block_size, num_blocks,
+ * k_/v_stride_*, new_kv_stride_*.
+ */
+int vaa_kv_write_slots(const vaa_attn_params* p, uint16_t* key_cache,
+                       uint16_t* value_cache, const void* slot_mapping,
+                       int slot_index_type, const uint16_t* new_keys,
+                       const uint16_t* new_values, int num_tokens,
+                       void* stream);
+
+/*
+ * Replaces kv_write_decode (vllm_apple/metal/kernels/paged_attention_fused.metal:55-101,
+ * guarded variant vllm_apple/engine/ops/kv_write.py:66-114, host
+ * KVWriteOp.encode_decode :261-334): the new token of sequence s is written
+ * at position seq_lens[s]-1 through block_table.  seq_len <= 0, a block index
+ * >= max_blocks_per_seq or an invalid physical block -> no write.
+ */
+int vaa_kv_write_decode(const vaa_attn_params* p, uint16_t* key_cache,
+                        uint16_t* value_cache, const int32_t* block_table,
+                        const int32_t* seq_lens, const uint16_t* new_keys,
+                        const uint16_t* new_values, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged attention
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Bytes of split-K workspace vaa_paged_attention_decode needs for these
+ * parameters (0 when every sequence fits one partition).  The partition size
+ * actually used is written to *partition_size_out when it is non-null.
+ */
+size_t vaa_paged_attention_decode_workspace_size(const vaa_attn_params* p,
+                                                 int32_t* partition_size_out);
+
+/*
+ * Paged decode attention with GQA.  Replaces paged_attention_fused_h128 /
+ * paged_attention_fused_generic (vllm_apple/metal/kernels/paged_attention_fused.metal:107-328),
+ * paged_attention_v2_decode[_h128] (paged_attention_v2.metal:49-261) and the
+ * host PagedAttentionOp.encode_decode_fused (vllm_apple/engine/ops/attention.py:369-537).
+ *
+ * For sequence s, query head h, kv head h / queries_per_kv:
+ *   out[s,h,:] = sum_{j < L} softmax_j(scale * q[s,h,:] . K_j) V_j,  L = seq_lens[s]
+ * with fp32 accumulation; seq_len <= 0 gives a zero row.  When new_keys and
+ * new_values are non-null the token at position L-1 is taken from them and
+ * written to the cache in the same launch (the fused KV write); when they are
+ * null the cache must already hold it.  Long contexts are split into
+ * partitions whose partial (max, sum, acc) are merged (log-sum-exp) by the
+ * last partition to finish, inside the same launch.  When split-K is used
+ * (workspace size > 0) the workspace must hold
+ * vaa_paged_attention_decode_workspace_size(p) bytes of scratch, and
+ * `counters` must point to num_seqs * num_kv_heads int32 that are zero before
+ * the call; every completed call leaves them zero, so one zero fill at
+ * allocation suffices.  The counters must be dedicated to this use and not
+ * shared by calls that can run concurrently.  Both may be null when every
+ * sequence fits one partition.
+ */
+int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
+                               uint16_t* key_cache, uint16_t* value_cache,
+                               const int32_t* block_table,
+                               const int32_t* seq_lens, uint16_t* output,
+                               const uint16_t* new_keys,
+                               const uint16_t* new_values, void* workspace,
+                               size_t workspace_bytes, int32_t* counters,
+                               void* stream);
+
+/*
+ * Chunked-prefill paged attention (MFMA).  Replaces paged_attention_v2_prefill
+ * (vllm_apple/metal/kernels/paged_attention_v2.metal:375-478, host
+ * PagedAttentionOp.encode_prefill vllm_apple/engine/ops/attention.py:290-367).
+ * Token t (query row t) of sequence token_to_seq[t] attends to cache
+ * positions [0, positions[t]] through that sequence's block table, so the
+ * cached prefix and the causal mask inside the chunk both follow from the
+ * positions.  The chunk's own K/V must already be in the cache.  Rows with
+ * an invalid sequence, a negative position, a context longer than the block
+ * table or an invalid block inside the context are left unwritten, as in the
+ * reference kernel.
+ */
+int vaa_paged_attention_prefill(const vaa_attn_params* p, const uint16_t* query,
+                                const uint16_t* key_cache,
+                                const uint16_t* value_cache,
+                                const int32_t* block_table,
+                                const int32_t* token_to_seq,
+                                const int32_t* positions, uint16_t* output,
+                                int num_tokens, void* stream);
+
+/*
+ * token_to_seq and positions for a flattened batch, computed on the device
+ * from query_start_loc [num_seqs+1] and full seq_lens [num_seqs]:
+ *   token_to_seq = repeat_interleave(arange(num_seqs), diff(query_start_loc))
+ *       (vllm_apple/engine/runner.py:526-546)
+ *   positions[t] = seq_lens[s] - query_len[s] + (t - query_start_loc[s])
+ *       (full seq_lens include the new tokens, apple_model_runner.py:1188-1200)
+ * Tokens outside [query_start_loc[0], query_start_loc[num_seqs]) get -1.
+ */
+int vaa_build_token_index(const int32_t* query_start_loc,
+                          const int32_t* seq_lens, int num_seqs,
+                          int num_tokens, int32_t* token_to_seq,
+                          int32_t* positions, void* stream);
+
+/*
+ * slot_mapping[t] = block_table[s, pos/bs]*bs + pos%bs for s = token_to_seq[t],
+ * pos = positions[t]; when the block index is past the table width or the
+ * entry is negative the slot is pos itself, as the reference runner does
+ * (vllm_apple/v1/worker/apple_model_runner.py:1202-1249).  Invalid s or
+ * negative pos -> -1.  Output is int64 (vLLM metadata type).
+ */
+int vaa_build_slot_mapping(const int32_t* block_table, int max_blocks_per_seq,
+                           int block_size, const int32_t* token_to_seq,
+                           const int32_t* positions, int num_seqs,
+                           int num_tokens, int64_t* slot_mapping,
+                           void* stream);
+
+/* ------------------------------------------------------------------------
+ * Layer ops next to attention
+ * ---------------------------------------------------------------------- */
+
+/*
+ * RMSNorm.  Replaces rmsnorm_kernel / rmsnorm_residual_kernel
+ * (vllm_apple/engine/ops/rmsnorm.py:78-173, host EngineRMSNorm.encode :226-321):
+ *   out = half(float(x) * rsqrt(mean(float(x)^2) + eps) * float(w)) [+ residual]
+ * The residual (may be null) is added after the norm, as the reference
+ * kernel does.  Row strides are in elements.
+ */
+int vaa_rmsnorm(const uint16_t* input, uint16_t* output, const uint16_t* weight,
+                const uint16_t* residual, int num_tokens, int hidden_size,
+                int64_t input_stride, int64_t output_stride,
+                int64_t residual_stride, float eps, void* stream);
+
+/*
+ * NeoX (split-half) rotary embedding, in place on query [T, num_heads, D] and
+ * key [T, num_kv_heads, D] (token strides given, heads contiguous at stride
+ * head_size).  Replaces rope_neox_kernel (vllm_apple/engine/ops/elementwise.py:185-239,
+ * host EngineRoPE.encode :699-766).  cos_cache/sin_cache are fp32
+ * [max_position, rotary_dim/2]; tokens whose position is outside
+ * [0, max_position) are left unrotated.  key may be null.
+ */
+int vaa_rope_neox(uint16_t* query, uint16_t* key, const float* cos_cache,
+                  const float* sin_cache, const int32_t* positions,
+                  int num_tokens, int num_heads, int num_kv_heads,
+                  int head_size, int rotary_dim, int64_t q_stride_token,
+                  int64_t k_stride_token, int max_position, void* stream);
+
+/*
+ * SwiGLU: out = half(silu(float(g)) * float(u)).  Replaces silu_mul_kernel
+ * (vllm_apple/engine/ops/elementwise.py:114-124, host encode_silu_mul
+ * :496-532) over num_elements contiguous elements.
+ */
+int vaa_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* output,
+                 int64_t num_elements, void* stream);
+
+/*
+ * Row-strided SwiGLU over [rows, cols] (e.g. gate/up halves of vLLM's
+ * [T, 2I] projection output).  Strides in elements.  No counterpart entry
+ * point in the reference; same arithmetic as vaa_silu_mul.
+ */
+int vaa_silu_mul_2d(const uint16_t* gate, const uint16_t* up, uint16_t* output,
+                    int64_t rows, int64_t cols, int64_t gate_stride,
+                    int64_t up_stride, int64_t output_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_APPLE_AMD_H_ */

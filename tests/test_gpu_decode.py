@@ -1,0 +1,149 @@
+"""Paged decode attention (fused KV write, GQA, split-K + LSE merge) vs the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, host
+
+import oracle.attention as oat
+import oracle.kv as okv
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(S, H, KV, D, lens, nb=None, bs=16, layout="kernel", seed=0, maxb=None):
+    g = torch.Generator().manual_seed(seed)
+    nblk = [(L + bs - 1) // bs for L in lens]
+    maxb = maxb or max(max(nblk), 1)
+    nb = nb or max(sum(nblk) + 4, 8)
+    shape = (nb, KV, bs, D) if layout == "kernel" else (nb, bs, KV, D)
+    kc = torch.randn(shape, generator=g).half()
+    vc = torch.randn(shape, generator=g).half()
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    bt = torch.full((S, maxb), -1, dtype=torch.int32)
+    off = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[off:off + n]
+        off += n
+    q = torch.randn(S, H, D, generator=g).half()
+    nk = torch.randn(S, KV, D, generator=g).half()
+    nv = torch.randn(S, KV, D, generator=g).half()
+    return kc, vc, bt, torch.tensor(lens, dtype=torch.int32), q, nk, nv
+
+
+def _run(kc, vc, bt, lens, q, nk, nv, *, layout="kernel", fused=True, part=0, scale=None):
+    from vllm_apple_amd import kernels
+
+    D = q.shape[2]
+    scale = scale or 1.0 / np.sqrt(D)
+    kd, vd = kc.cuda(), vc.cuda()
+    out = kernels.paged_decode(q.cuda(), kd, vd, bt.cuda(), lens.cuda(), scale=scale,
+                               max_seq_len=int(lens.max()) if lens.numel() else 0,
+                               layout=layout, new_keys=nk.cuda() if fused else None,
+                               new_values=nv.cuda() if fused else None, partition_size=part)
+    torch.cuda.synchronize()
+    # Oracle: write the new token first (when fused), then attend.
+    kc_ref, vc_ref = host(kc).copy(), host(vc).copy()
+    if fused:
+        okv.kv_write_decode(kc_ref, vc_ref, host(nk), host(nv), host(bt), host(lens), layout)
+    ref = oat.decode(host(q), kc_ref, vc_ref, host(bt), host(lens), scale, layout)
+    return out, ref, kd, vd, kc_ref, vc_ref
+
+
+@pytest.mark.parametrize("part", [0, 64, 128, 512])
+def test_decode_c1_shape(gpu, part):
+    """C1 shape (14q/2kv, D64, GQA 7), fused write, several partition sizes."""
+    lens = [37, 512, 16, 201]
+    print(f"[case] C1 part={part}", flush=True)
+    kc, vc, bt, L, q, nk, nv = _case(4, 14, 2, 64, lens, nb=256, seed=1, maxb=32)
+    out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=part, scale=1 / 8)
+    assert_close(host(out), ref, what="decode C1")
+    assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16)), "fused K write"
+    assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16)), "fused V write"
+
+
+@pytest.mark.parametrize("layout", ["kernel", "vllm"])
+def test_decode_c2_shape_uniform(gpu, layout):
+    """C2 shape (32q/8kv, D128) with U{1024..8192} contexts, 6 sequences."""
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(1024, 8193, (6,), generator=g).tolist()
+    print(f"[case] C2 layout={layout} lens={lens}", flush=True)
+    kc, vc, bt, L, q, nk, nv = _case(6, 32, 8, 128, lens, seed=2, layout=layout)
+    out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, layout=layout)
+    assert_close(host(out), ref, what=f"decode C2 {layout}")
+    assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
+    assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16))
+
+
+@pytest.mark.parametrize("D", [32, 64, 96, 128])
+@pytest.mark.parametrize("H,KV", [(8, 8), (16, 4), (16, 2), (32, 2), (16, 1)])
+def test_decode_head_shapes(gpu, D, H, KV):
+    lens = [1, 15, 16, 17, 300, 1000]
+    print(f"[case] shapes D={D} H={H} KV={KV}", flush=True)
+    kc, vc, bt, L, q, nk, nv = _case(6, H, KV, D, lens, seed=3)
+    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=128)
+    assert_close(host(out), ref, what=f"decode D={D} H={H} KV={KV}")
+
+
+def test_decode_unfused_reads_cache(gpu):
+    lens = [100, 2000, 33]
+    kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, lens, seed=4)
+    out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, fused=False)
+    assert_close(host(out), ref, what="decode unfused")
+    assert np.array_equal(host(kd).view(np.uint16), host(kc).view(np.uint16))
+
+
+def test_decode_seq_len_one_is_value_exact(gpu):
+    """Known answer (tests/metal/test_metal_kernels.py:380-438): L=1 -> new V per GQA group."""
+    kc, vc, bt, L, q, nk, nv = _case(1, 32, 4, 64, [1], nb=8, seed=5)
+    out, *_ = _run(kc, vc, bt, L, q, nk, nv)
+    expected = nv.repeat_interleave(8, dim=1)
+    assert torch.equal(out.cpu(), expected)
+
+
+def test_decode_zero_and_edge_lengths(gpu):
+    lens = [0, 1, 16, 0, 4097]
+    kc, vc, bt, L, q, nk, nv = _case(5, 16, 4, 128, lens, seed=6)
+    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=256)
+    assert_close(host(out), ref, what="decode edge lengths")
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[3]) == 0
+
+
+def test_decode_split_matches_unsplit(gpu):
+    lens = [5000, 3000, 7777]
+    kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, lens, seed=7)
+    a, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=64)
+    b, *_ = _run(kc, vc, bt, L, q, nk, nv, part=8192)
+    assert_close(host(a), ref, what="split 64")
+    assert_close(host(b), ref, what="split 8192")
+    assert_close(host(a), host(b).astype(np.float64), what="split vs unsplit")
+
+
+def test_decode_outlier_keys_c4_style(gpu):
+    """1% of key rows x8 (C4): softmax max-tracking across partitions."""
+    lens = [9000, 4096, 12000]
+    kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, lens, seed=8)
+    g = torch.Generator().manual_seed(9)
+    flat = kc.view(-1, 128)
+    idx = torch.randint(0, flat.shape[0], (flat.shape[0] // 100,), generator=g)
+    flat[idx] = (flat[idx].float() * 8).half()
+    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=512)
+    assert_close(host(out), ref, what="decode outliers")
+
+
+def test_decode_invalid_block_is_masked(gpu):
+    lens = [64, 64]
+    kc, vc, bt, L, q, nk, nv = _case(2, 8, 2, 64, lens, seed=10)
+    bt[0, 1] = -1
+    bt[1, 2] = 10_000  # past capacity
+    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, fused=False)
+    assert_close(host(out), ref, what="decode invalid blocks")
+
+
+def test_decode_matches_pure_loop_oracle(gpu):
+    """Small case against the token-serial fp32 loop that mirrors the Metal kernel."""
+    lens = [45, 7]
+    kc, vc, bt, L, q, nk, nv = _case(2, 4, 2, 32, lens, seed=12)
+    out, *_ = _run(kc, vc, bt, L, q, nk, nv, fused=False)
+    loop = oat.decode_loop_fp32(host(q), host(kc), host(vc), host(bt), host(L), 1 / np.sqrt(32))
+    assert_close(host(out), loop, what="vs Metal-structured loop")

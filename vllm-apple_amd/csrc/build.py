@@ -1,0 +1,89 @@
+"""Build libvllm_apple_amd.so for gfx950 with hipcc.
+
+Each .hip file is compiled to an object in parallel, then linked into one
+shared library placed next to the Python package, in-tree, so it ships with
+the source tree.  Run directly (``python build.py``) or through
+``vllm_apple_amd.build_library()``.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PKG_ROOT = HERE.parent                      # vllm-apple_amd/
+REPO = PKG_ROOT.parent                      # repository root
+INCLUDE = REPO / "include"
+OUT_DIR = PKG_ROOT / "vllm_apple_amd"
+LIB_NAME = "libvllm_apple_amd.so"
+OBJ_DIR = PKG_ROOT / "_build"
+
+SOURCES = [
+    "status.hip",
+    "kv_write.hip",
+    "paged_decode.hip",
+    "paged_prefill.hip",
+    "layer_ops.hip",
+    "index_ops.hip",
+]
+
+ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def common_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-Wall",
+        "-Wno-unused-function",
+        f"-I{INCLUDE}",
+        f"-I{HERE}",
+        # Keep hipcc from emitting packed-fp32 VALU ops.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    ]
+
+
+def _compile(src: str) -> Path:
+    obj = OBJ_DIR / (Path(src).stem + ".o")
+    cmd = [hipcc(), *common_flags(), "-c", str(HERE / src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+    if err.strip():
+        sys.stderr.write(err + "\n")
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    out = OUT_DIR / LIB_NAME
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
+if __name__ == "__main__":
+    build()

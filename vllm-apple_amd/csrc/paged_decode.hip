@@ -1,0 +1,532 @@
+// Paged decode attention for gfx950 (CDNA4), GQA, split-K with a log-sum-exp
+// merge, optional fused write of the new token's K/V.
+//
+// Reference semantics: paged_attention_fused.metal:107-328 and
+// paged_attention_v2.metal:49-261 (online softmax in fp32 over the first
+// seq_len cache positions of the sequence, kv head = q head / queries_per_kv,
+// zero row for seq_len <= 0).
+//
+// Work decomposition
+//   grid  = (partition, kv_head, seq); one workgroup serves every query head
+//           of the GQA group, so each K/V byte is read from HBM once.
+//   block = 4 waves; the partition's 16-token tiles are split between them and
+//           each wave keeps its own (max, sum, acc) until a final LDS combine.
+//   split-K = partitions of 512 tokens by default; partials (max, sum, acc) go
+//           to the workspace and the last partition of a (seq, kv_head) to
+//           finish merges them (log-sum-exp) in the same launch.
+//
+// Per 16-token tile a wave does
+//   S^T[16 tok x 16 heads] = K[16 x D] * Q^T[D x 16]   (D/32 x mfma 16x16x32)
+//   P = exp2(S*scale*log2e - m)                         (fp32, heads on lanes)
+//   O^T[D x 16 heads]     += V^T[D x 16] * P^T[16 x 16] (D/16 x mfma 16x16x16)
+// Heads >= queries_per_kv are zero columns.  S^T (not S) is computed so the
+// MFMA output layout (lane = head, 4 tokens per lane) is exactly the B operand
+// layout of the PV product and the per-head softmax statistics live in the
+// same lanes as the head's accumulators: no shuffles besides the 2-step
+// cross-lane max.
+//
+// Memory: each lane loads 16-byte pieces of one K row straight into the MFMA
+// A-operand registers (the contraction index d is permuted identically in K
+// and Q).  V is loaded with fully coalesced 16-byte loads, stored to a per-wave
+// LDS tile (XOR-swizzled 16-byte chunks) and read back transposed.
+#include "common.h"
+
+namespace vaa {
+namespace {
+
+constexpr int kDecodeWaves = 4;
+constexpr int kTile = 16;  // tokens per MFMA tile
+
+struct DecodeArgs {
+  const f16* q;
+  f16* kc;
+  f16* vc;
+  const int32_t* bt;
+  const int32_t* seq_lens;
+  f16* out;
+  const f16* new_k;
+  const f16* new_v;
+  float* ws_acc;  // [seq][qhead][part][D] unnormalised partial outputs
+  float* ws_ml;   // [seq][qhead][part][2] (max in log2 domain, sum)
+  int* ws_cnt;    // [seq][kv_head] finished-partition counters (zero between calls)
+                  // (a dedicated caller buffer, never part of the partials)
+  float scale_log2;
+  int num_seqs, max_blocks, block_size, num_kv_heads, num_q_heads, G;
+  int part_tiles, max_parts;
+  int64_t num_blocks;
+  int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+  int64_t q_st, q_sh, o_st, o_sh, n_st, n_sh;
+};
+
+template <int D>
+struct Cfg {
+  static constexpr int NS = D / 32;       // QK mfma count (K-dim 32)
+  static constexpr int NDT = D / 16;      // PV mfma count (16 output dims each)
+  static constexpr int CH = D / 8;        // 16-byte chunks per row
+  static constexpr int VLD = kTile * CH / kWave;  // V loads per lane per tile
+  static constexpr bool SWZ = (CH == 8 || CH == 16);
+};
+
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (Cfg<D>::SWZ) return ((row >> 2) & 3) << 1;
+  return 0;
+}
+
+template <int D>
+struct TileRegs {
+  u32x4 k[Cfg<D>::NS];
+  u32x4 v[Cfg<D>::VLD];
+  int vsti;  // index of the V chunk holding the new token (fused write), or -1
+};
+
+// Issue the loads of tile j (16 tokens) for this lane.  valid_rows is the
+// number of real tokens in the tile (0 for an invalid block).
+template <int D>
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, int seq, int kvh,
+                                          int L, int j, int lane, int new_row,
+                                          TileRegs<D>& r, int& valid_rows,
+                                          f16*& kst, f16*& vst) {
+  const int tok0 = j * kTile;
+  const int bi = tok0 / a.block_size;
+  const int row0 = tok0 - bi * a.block_size;
+  int64_t phys = a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi];
+  valid_rows = min(kTile, L - tok0);
+  if (phys < 0 || phys >= a.num_blocks) {
+    phys = 0;
+    valid_rows = 0;
+  }
+  const f16* kb = a.kc + phys * a.k_sb + kvh * a.k_sh + row0 * a.k_st;
+  const f16* vb = a.vc + phys * a.v_sb + kvh * a.v_sh + row0 * a.v_st;
+  const int c16 = lane & 15, g = lane >> 4;
+  // K: row c16, NS contiguous 16-byte pieces starting at element g*D/4.
+  const f16* kp = kb + c16 * a.k_st + g * (D / 4);
+  kst = nullptr;
+  if (c16 == new_row && valid_rows > 0) {
+    kst = const_cast<f16*>(kp);
+    kp = a.new_k + seq * a.n_st + kvh * a.n_sh + g * (D / 4);
+  }
+#pragma unroll
+  for (int s = 0; s < Cfg<D>::NS; ++s) r.k[s] = ld16(kp + 8 * s);
+  // V: coalesced; flat chunk f = i*64 + lane -> (row f/CH, chunk f%CH).
+  vst = nullptr;
+  r.vsti = -1;
+#pragma unroll
+  for (int i = 0; i < Cfg<D>::VLD; ++i) {
+    const int f = i * kWave + lane;
+    const int row = f / Cfg<D>::CH, ch = f % Cfg<D>::CH;
+    const f16* vp = vb + row * a.v_st + ch * 8;
+    if (row == new_row && valid_rows > 0) {
+      vst = const_cast<f16*>(vp);  // cache slot of this chunk
+      r.vsti = i;
+      vp = a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8;
+    }
+    r.v[i] = ld16(vp);
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(kDecodeWaves* kWave)
+paged_decode_kernel(DecodeArgs a) {
+  using C = Cfg<D>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int G = a.G;
+
+  int L = a.seq_lens[seq];
+  const int Lorig = L;
+  const int cap = a.max_blocks * a.block_size;
+  if (L > cap) L = cap;
+  if (L <= 0) {
+    if (part == 0) {
+      for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+        const int h = kvh * G + idx / D;
+        a.out[seq * a.o_st + h * a.o_sh + idx % D] = f2h(0.f);
+      }
+    }
+    return;
+  }
+  const int part_tok = a.part_tiles * kTile;
+  const int n_tiles = (L + kTile - 1) / kTile;
+  const int n_parts = min((L + part_tok - 1) / part_tok, a.max_parts);
+  if (part >= n_parts) return;
+  const int t0 = part * a.part_tiles;
+  const int t1 = (part == a.max_parts - 1) ? n_tiles : min(t0 + a.part_tiles, n_tiles);
+  const int per = (t1 - t0 + kDecodeWaves - 1) / kDecodeWaves;
+  const int jb = t0 + wave * per;
+  const int je = min(jb + per, t1);
+
+  // Row of the new token inside the last tile (fused KV write), else -1.
+  int new_row_last = -1;
+  if (a.new_k != nullptr && Lorig == L) new_row_last = (L - 1) - (n_tiles - 1) * kTile;
+
+  // Q^T as the B operand: lane holds Q[head c16][g*D/4 + 8s .. +7].
+  u32x4 qb[C::NS];
+  {
+    const bool hv = c16 < G;
+    const f16* qp = a.q + seq * a.q_st + (kvh * G + (hv ? c16 : 0)) * a.q_sh + g * (D / 4);
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+      qb[s] = hv ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  f16* vt = reinterpret_cast<f16*>(smem) + wave * (kTile * D);
+  float m_run = -INFINITY, l_part = 0.f;
+  f32x4 acc[C::NDT];
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (jb < je) {
+    TileRegs<D> cur;
+    int cur_valid;
+    f16 *cur_kst, *cur_vst;
+    load_tile<D>(a, seq, kvh, L, jb, lane, jb == n_tiles - 1 ? new_row_last : -1,
+                 cur, cur_valid, cur_kst, cur_vst);
+    for (int j = jb; j < je; ++j) {
+      TileRegs<D> nxt;
+      int nxt_valid = 0;
+      f16 *nxt_kst = nullptr, *nxt_vst = nullptr;
+      if (j + 1 < je)
+        load_tile<D>(a, seq, kvh, L, j + 1, lane,
+                     j + 1 == n_tiles - 1 ? new_row_last : -1, nxt, nxt_valid,
+                     nxt_kst, nxt_vst);
+
+      // Fused KV write: the lanes that hold the new token store it.
+      if (cur_kst) {
+#pragma unroll
+        for (int s = 0; s < C::NS; ++s) st16(cur_kst + 8 * s, cur.k[s]);
+      }
+      if (cur_vst) {
+#pragma unroll
+        for (int i = 0; i < C::VLD; ++i)
+          if (i == cur.vsti) st16(cur_vst, cur.v[i]);
+      }
+
+      // V tile -> LDS (rows past the sequence end are zeroed so stale cache
+      // contents can never reach the accumulators).
+#pragma unroll
+      for (int i = 0; i < C::VLD; ++i) {
+        const int f = i * kWave + lane;
+        const int row = f / C::CH, ch = f % C::CH;
+        u32x4 v = row < cur_valid ? cur.v[i] : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(vt + row * D + ((ch ^ swz<D>(row)) * 8)) = v;
+      }
+
+      // S^T = K Q^T.
+      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < C::NS; ++s) {
+        s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(f16x8, cur.k[s]), __builtin_bit_cast(f16x8, qb[s]),
+            s4, 0, 0, 0);
+      }
+      // Online softmax (log2 domain); lane = head c16, tokens 4g..4g+3.
+      float x[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = (4 * g + r < cur_valid) ? s4[r] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, x[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
+      const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;
+      f16x4 ph;
+      float psum = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ph[r] = f2h(fast_exp2(x[r] - m_sub));
+        psum += h2f(ph[r]);
+      }
+      l_part = l_part * alpha + psum;
+      m_run = m_new;
+      if (alpha != 1.f) {
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
+      }
+
+      // O^T += V^T P^T; lane reads V[4g+r][16dt + c16] from LDS.
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        const int d = 16 * dt + c16;
+        f16x4 va;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 4 * g + r;
+          va[r] = vt[row * D + (((d >> 3) ^ swz<D>(row)) * 8) + (d & 7)];
+        }
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc[dt], 0, 0, 0);
+      }
+
+      cur = nxt;
+      cur_valid = nxt_valid;
+      cur_kst = nxt_kst;
+      cur_vst = nxt_vst;
+    }
+  }
+
+  // Sum over the four token groups of this head.
+  l_part += __shfl_xor(l_part, 16, kWave);
+  l_part += __shfl_xor(l_part, 32, kWave);
+
+  // Cross-wave combine through LDS: wm/wl [wave][G], wa [wave][G][D].
+  __syncthreads();
+  float* wm = reinterpret_cast<float*>(smem);
+  float* wl = wm + kDecodeWaves * 16;
+  float* wa = wl + kDecodeWaves * 16;
+  if (c16 < G) {
+    if (g == 0) {
+      wm[wave * 16 + c16] = m_run;
+      wl[wave * 16 + c16] = l_part;
+    }
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * dt + 4 * g + r;
+        wa[(wave * G + c16) * D + d] = acc[dt][r];
+      }
+    }
+  }
+  __syncthreads();
+
+  const int H = a.num_q_heads;
+  const bool single = (n_parts == 1);
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int h = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, wm[w * 16 + h]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecodeWaves; ++w) {
+        const float mw = wm[w * 16 + h];
+        if (mw == -INFINITY) continue;
+        const float sc = fast_exp2(mw - M);
+        num += sc * wa[(w * G + h) * D + d];
+        den += sc * wl[w * 16 + h];
+      }
+    }
+    const int qh = kvh * G + h;
+    if (single) {
+      a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
+    } else {
+      const int64_t row = (static_cast<int64_t>(seq) * H + qh) * a.max_parts + part;
+      a.ws_acc[row * D + d] = num;
+      if (d == 0) {
+        a.ws_ml[row * 2 + 0] = M;
+        a.ws_ml[row * 2 + 1] = den;
+      }
+    }
+  }
+  if (single) return;
+
+  // Split-K merge by the last partition to finish for this (seq, kv_head):
+  // out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.  No workgroup ever
+  // waits: the others simply exit.  Agent-scope fences order the partials
+  // (written on any XCD) before the counter and the counter before the reads.
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* cnt = a.ws_cnt + static_cast<int64_t>(seq) * a.num_kv_heads + kvh;
+    const int prev = atomicAdd(cnt, 1);
+    s_last = (prev == n_parts - 1);
+    if (s_last) atomicExch(cnt, 0);  // leave the counter at zero for the next call
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int h = idx / D, d = idx % D;
+    const int qh = kvh * G + h;
+    const int64_t row0 = (static_cast<int64_t>(seq) * H + qh) * a.max_parts;
+    float M = -INFINITY;
+    for (int p = 0; p < n_parts; ++p) {
+      if (a.ws_ml[(row0 + p) * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[(row0 + p) * 2]);
+    }
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+      for (int p = 0; p < n_parts; ++p) {
+        const float lp = a.ws_ml[(row0 + p) * 2 + 1];
+        if (!(lp > 0.f)) continue;
+        const float sc = fast_exp2(a.ws_ml[(row0 + p) * 2] - M);
+        num += sc * a.ws_acc[(row0 + p) * D + d];
+        den += sc * lp;
+      }
+    }
+    a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
+  }
+}
+
+int choose_partition(const vaa_attn_params* p, int* part_out, int* max_parts_out) {
+  const int64_t cap = static_cast<int64_t>(p->max_blocks_per_seq) * p->block_size;
+  int64_t max_len = p->max_seq_len;
+  if (max_len > cap) max_len = cap;
+  if (max_len < 1) max_len = 1;
+  int part = p->partition_size;
+  if (part > 0) {
+    if (part % (kTile * kDecodeWaves) != 0)
+      return fail(VAA_ERR_INVALID_ARG,
+                  "partition_size=%d must be a positive multiple of %d", part,
+                  kTile * kDecodeWaves);
+  } else {
+    const int64_t pairs = static_cast<int64_t>(p->num_seqs) * p->num_kv_heads;
+    part = 512;
+    while (part > kTile * kDecodeWaves &&
+           pairs * ((max_len + part - 1) / part) < 1024)
+      part /= 2;
+  }
+  *part_out = part;
+  *max_parts_out = static_cast<int>((max_len + part - 1) / part);
+  return VAA_OK;
+}
+
+int check_params(const vaa_attn_params* p, const char* what) {
+  if (!p) return fail(VAA_ERR_INVALID_ARG, "%s: null params", what);
+  if (p->head_size != 32 && p->head_size != 64 && p->head_size != 96 &&
+      p->head_size != 128)
+    return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d not in {32,64,96,128}",
+                what, p->head_size);
+  if (p->block_size <= 0 || p->block_size % kTile != 0)
+    return fail(VAA_ERR_UNSUPPORTED, "%s: block_size=%d must be a multiple of 16",
+                what, p->block_size);
+  if (p->num_kv_heads <= 0 || p->num_query_heads <= 0 ||
+      p->num_query_heads % p->num_kv_heads != 0 ||
+      p->queries_per_kv != p->num_query_heads / p->num_kv_heads)
+    return fail(VAA_ERR_INVALID_ARG, "%s: heads %d/%d, queries_per_kv=%d", what,
+                p->num_query_heads, p->num_kv_heads, p->queries_per_kv);
+  if (p->queries_per_kv > 16)
+    return fail(VAA_ERR_UNSUPPORTED, "%s: queries_per_kv=%d > 16", what,
+                p->queries_per_kv);
+  if (p->num_seqs < 0 || p->max_blocks_per_seq <= 0 || p->num_blocks <= 0)
+    return fail(VAA_ERR_INVALID_ARG,
+                "%s: num_seqs=%d max_blocks_per_seq=%d num_blocks=%lld", what,
+                p->num_seqs, p->max_blocks_per_seq, (long long)p->num_blocks);
+  const int64_t strides[] = {p->k_stride_block, p->k_stride_head, p->k_stride_token,
+                             p->v_stride_block, p->v_stride_head, p->v_stride_token,
+                             p->q_stride_token, p->q_stride_head, p->o_stride_token,
+                             p->o_stride_head};
+  for (int64_t s : strides)
+    if (s < 0 || s % 8 != 0)
+      return fail(VAA_ERR_INVALID_ARG,
+                  "%s: strides must be non-negative multiples of 8 elements", what);
+  return VAA_OK;
+}
+
+template <int D>
+int launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream) {
+  const size_t lds_tiles = static_cast<size_t>(kDecodeWaves) * kTile * D * sizeof(f16);
+  const size_t lds_comb =
+      (2 * kDecodeWaves * 16 + static_cast<size_t>(kDecodeWaves) * a.G * D) * sizeof(float);
+  const size_t lds = lds_tiles > lds_comb ? lds_tiles : lds_comb;
+  dim3 grid(a.max_parts, a.num_kv_heads, num_seqs);
+  hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kDecodeWaves * kWave), lds,
+                     stream, a);
+  return check_launch("paged_decode_kernel");
+}
+
+}  // namespace
+}  // namespace vaa
+
+using namespace vaa;
+
+extern "C" size_t vaa_paged_attention_decode_workspace_size(const vaa_attn_params* p,
+                                                            int32_t* partition_size_out) {
+  if (!p || p->num_seqs <= 0 || p->block_size <= 0 || p->max_blocks_per_seq <= 0)
+    return 0;
+  int part, max_parts;
+  if (choose_partition(p, &part, &max_parts) != VAA_OK) return 0;
+  if (partition_size_out) *partition_size_out = part;
+  if (max_parts <= 1) return 0;
+  return static_cast<size_t>(p->num_seqs) * p->num_query_heads * max_parts *
+         (p->head_size + 2) * sizeof(float);
+}
+
+extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
+                                          const uint16_t* query,
+                                          uint16_t* key_cache,
+                                          uint16_t* value_cache,
+                                          const int32_t* block_table,
+                                          const int32_t* seq_lens,
+                                          uint16_t* output,
+                                          const uint16_t* new_keys,
+                                          const uint16_t* new_values,
+                                          void* workspace, size_t workspace_bytes,
+                                          int32_t* counters, void* stream) {
+  int st = check_params(p, "vaa_paged_attention_decode");
+  if (st) return st;
+  if (p->num_seqs == 0) return VAA_OK;
+  if (!query || !key_cache || !value_cache || !block_table || !seq_lens || !output)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_paged_attention_decode: null pointer");
+  if ((new_keys == nullptr) != (new_values == nullptr))
+    return fail(VAA_ERR_INVALID_ARG,
+                "vaa_paged_attention_decode: new_keys and new_values go together");
+  if (new_keys && (p->new_kv_stride_token % 8 || p->new_kv_stride_head % 8 ||
+                   !aligned16(new_keys) || !aligned16(new_values)))
+    return fail(VAA_ERR_INVALID_ARG,
+                "vaa_paged_attention_decode: new K/V must be 16-byte aligned rows");
+  if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache))
+    return fail(VAA_ERR_INVALID_ARG,
+                "vaa_paged_attention_decode: query and caches must be 16-byte aligned");
+  int part, max_parts;
+  st = choose_partition(p, &part, &max_parts);
+  if (st) return st;
+
+  DecodeArgs a;
+  a.q = reinterpret_cast<const f16*>(query);
+  a.kc = reinterpret_cast<f16*>(key_cache);
+  a.vc = reinterpret_cast<f16*>(value_cache);
+  a.bt = block_table;
+  a.seq_lens = seq_lens;
+  a.out = reinterpret_cast<f16*>(output);
+  a.new_k = reinterpret_cast<const f16*>(new_keys);
+  a.new_v = reinterpret_cast<const f16*>(new_values);
+  a.ws_acc = nullptr;
+  a.ws_ml = nullptr;
+  a.ws_cnt = nullptr;
+  if (max_parts > 1) {
+    const size_t need = vaa_paged_attention_decode_workspace_size(p, nullptr);
+    if (!workspace || workspace_bytes < need)
+      return fail(VAA_ERR_WORKSPACE,
+                  "vaa_paged_attention_decode: workspace %zu bytes < %zu needed",
+                  workspace_bytes, need);
+    if (!counters)
+      return fail(VAA_ERR_WORKSPACE,
+                  "vaa_paged_attention_decode: split-K needs the zeroed counters buffer");
+    const size_t rows = static_cast<size_t>(p->num_seqs) * p->num_query_heads * max_parts;
+    a.ws_acc = static_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + rows * p->head_size;
+    a.ws_cnt = counters;
+  }
+  a.scale_log2 = p->scale * kLog2e;
+  a.num_seqs = p->num_seqs;
+  a.max_blocks = p->max_blocks_per_seq;
+  a.block_size = p->block_size;
+  a.num_kv_heads = p->num_kv_heads;
+  a.num_q_heads = p->num_query_heads;
+  a.G = p->queries_per_kv;
+  a.part_tiles = part / kTile;
+  a.max_parts = max_parts;
+  a.num_blocks = p->num_blocks;
+  a.k_sb = p->k_stride_block; a.k_sh = p->k_stride_head; a.k_st = p->k_stride_token;
+  a.v_sb = p->v_stride_block; a.v_sh = p->v_stride_head; a.v_st = p->v_stride_token;
+  a.q_st = p->q_stride_token; a.q_sh = p->q_stride_head;
+  a.o_st = p->o_stride_token; a.o_sh = p->o_stride_head;
+  a.n_st = p->new_kv_stride_token; a.n_sh = p->new_kv_stride_head;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (p->head_size) {
+    case 32: return launch_decode<32>(a, p->num_seqs, s);
+    case 64: return launch_decode<64>(a, p->num_seqs, s);
+    case 96: return launch_decode<96>(a, p->num_seqs, s);
+    case 128: return launch_decode<128>(a, p->num_seqs, s);
+  }
+  return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
+}

@@ -1,0 +1,452 @@
+"""Functional wrappers over the HIP C ABI, taking torch tensors on the GPU.
+
+Every function enqueues work on torch's current HIP stream (or ``stream``) and
+returns without synchronising.  Arguments are checked on the host; tensors
+must live on a ROCm device -- there is no CPU fallback.
+
+KV caches are described by a layout name:
+  "kernel": K, V each [num_blocks, num_kv_heads, block_size, head_size]
+            (vllm_apple/metal/kv_cache.py:213-219)
+  "vllm":   K = kv_cache[0], V = kv_cache[1], each [num_blocks, block_size,
+            num_kv_heads, head_size] (metal_attn.py:171-185)
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+LAYOUTS = ("kernel", "vllm")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(
+                f"tensor on {t.device}: the HIP path needs ROCm device tensors "
+                "(there is no CPU fallback)")
+
+
+def _require_dtype(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+@dataclass(frozen=True)
+class CacheStrides:
+    num_blocks: int
+    block_size: int
+    num_kv_heads: int
+    head_size: int
+    stride_block: int
+    stride_head: int
+    stride_token: int
+
+
+def cache_strides(cache: torch.Tensor, layout: str) -> CacheStrides:
+    """Element strides of one K or V cache tensor in the given layout."""
+    if cache.dim() != 4:
+        raise ValueError(f"cache must be 4-D, got shape {tuple(cache.shape)}")
+    if cache.stride(3) != 1:
+        raise ValueError("cache head_size dimension must be contiguous")
+    if layout == "kernel":
+        nb, kv, bs, d = cache.shape
+        sb, sh, st = cache.stride(0), cache.stride(1), cache.stride(2)
+    elif layout == "vllm":
+        nb, bs, kv, d = cache.shape
+        sb, st, sh = cache.stride(0), cache.stride(1), cache.stride(2)
+    else:
+        raise ValueError(f"layout must be one of {LAYOUTS}, got {layout!r}")
+    return CacheStrides(nb, bs, kv, d, sb, sh, st)
+
+
+def make_params(*, key_cache: torch.Tensor, value_cache: torch.Tensor, layout: str,
+                num_query_heads: int, scale: float, num_seqs: int = 0,
+                max_seq_len: int = 0, max_blocks_per_seq: int = 0,
+                query: torch.Tensor | None = None, output: torch.Tensor | None = None,
+                new_kv: torch.Tensor | None = None,
+                partition_size: int = 0) -> _lib.VaaAttnParams:
+    ks = cache_strides(key_cache, layout)
+    vs = cache_strides(value_cache, layout)
+    if (ks.num_blocks, ks.block_size, ks.num_kv_heads, ks.head_size) != (
+            vs.num_blocks, vs.block_size, vs.num_kv_heads, vs.head_size):
+        raise ValueError("key and value caches differ in shape")
+    if num_query_heads % ks.num_kv_heads != 0:
+        raise ValueError(
+            f"num_query_heads={num_query_heads} not a multiple of num_kv_heads={ks.num_kv_heads}")
+    p = _lib.VaaAttnParams()
+    p.scale = float(scale)
+    p.num_seqs = int(num_seqs)
+    p.max_seq_len = int(max_seq_len)
+    p.max_blocks_per_seq = int(max_blocks_per_seq)
+    p.head_size = ks.head_size
+    p.block_size = ks.block_size
+    p.num_kv_heads = ks.num_kv_heads
+    p.num_query_heads = int(num_query_heads)
+    p.queries_per_kv = int(num_query_heads) // ks.num_kv_heads
+    p.partition_size = int(partition_size)
+    p.num_blocks = ks.num_blocks
+    p.k_stride_block, p.k_stride_head, p.k_stride_token = ks.stride_block, ks.stride_head, ks.stride_token
+    p.v_stride_block, p.v_stride_head, p.v_stride_token = vs.stride_block, vs.stride_head, vs.stride_token
+    for t, pre in ((query, "q"), (output, "o"), (new_kv, "new_kv")):
+        if t is None:
+            continue
+        if t.dim() != 3 or t.stride(2) != 1:
+            raise ValueError(f"{pre} tensor must be [tokens, heads, head_size] with contiguous last dim")
+        setattr(p, f"{pre}_stride_token", t.stride(0))
+        setattr(p, f"{pre}_stride_head", t.stride(1))
+    return p
+
+
+# ------------------------------------------------------------------ KV write
+
+
+def kv_write_slots(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                   value_cache: torch.Tensor, slot_mapping: torch.Tensor, *,
+                   layout: str = "kernel", stream=None) -> None:
+    """cache[slot // bs, :, slot % bs] = key/value[t] for every slot >= 0.
+
+    key/value: [num_tokens, num_kv_heads, head_size] fp16 (any token/head
+    strides with a contiguous last dim); slot_mapping: int32 or int64
+    [num_tokens].  Mirrors kv_write.py:118-156 and base_attn.py:308-342.
+    """
+    _require_gpu(key, value, key_cache, value_cache, slot_mapping)
+    for t, n in ((key, "key"), (value, "value"), (key_cache, "key_cache"), (value_cache, "value_cache")):
+        _require_dtype(t, torch.float16, n)
+    if key.stride() != value.stride() or key.shape != value.shape:
+        raise ValueError("key and value must have identical shapes and strides")
+    if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be a contiguous int32/int64 tensor")
+    n = key.shape[0]
+    if slot_mapping.numel() < n:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries < {n} tokens")
+    p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
+                    num_query_heads=key.shape[1], scale=1.0, new_kv=key)
+    if key.shape[1:] != (p.num_kv_heads, p.head_size):
+        raise ValueError(f"key shape {tuple(key.shape)} does not match the cache")
+    itype = _lib.VAA_INDEX_I64 if slot_mapping.dtype == torch.int64 else _lib.VAA_INDEX_I32
+    _lib.call("vaa_kv_write_slots", ctypes.byref(p), key_cache.data_ptr(), value_cache.data_ptr(),
+              slot_mapping.data_ptr(), itype, key.data_ptr(), value.data_ptr(), n,
+              _lib.stream_handle(stream))
+
+
+def kv_write_decode(new_keys: torch.Tensor, new_values: torch.Tensor, key_cache: torch.Tensor,
+                    value_cache: torch.Tensor, block_table: torch.Tensor,
+                    seq_lens: torch.Tensor, *, layout: str = "kernel", stream=None) -> None:
+    """Write each sequence's new token at position seq_lens[s]-1 (kv_write.py:66-114)."""
+    _require_gpu(new_keys, new_values, key_cache, value_cache, block_table, seq_lens)
+    _check_tables(block_table, seq_lens)
+    if new_keys.stride() != new_values.stride() or new_keys.shape != new_values.shape:
+        raise ValueError("new_keys and new_values must have identical shapes and strides")
+    num_seqs = seq_lens.numel()
+    p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
+                    num_query_heads=new_keys.shape[1], scale=1.0, num_seqs=num_seqs,
+                    max_blocks_per_seq=block_table.shape[1], new_kv=new_keys)
+    if new_keys.shape[0] < num_seqs:
+        raise ValueError("new_keys has fewer rows than sequences")
+    _lib.call("vaa_kv_write_decode", ctypes.byref(p), key_cache.data_ptr(), value_cache.data_ptr(),
+              block_table.data_ptr(), seq_lens.data_ptr(), new_keys.data_ptr(),
+              new_values.data_ptr(), _lib.stream_handle(stream))
+
+
+def write_kv_batch(key_dst: torch.Tensor, value_dst: torch.Tensor, key_src: torch.Tensor,
+                   value_src: torch.Tensor, block_ids: torch.Tensor,
+                   token_offsets: torch.Tensor, stride_block: int, stride_head: int,
+                   stride_token: int, num_blocks: int, stream=None) -> None:
+    """Device counterpart of metal_write_kv_batch (kv_write.c:33-78)."""
+    _require_gpu(key_dst, value_dst, key_src, value_src, block_ids, token_offsets)
+    if not (key_src.is_contiguous() and value_src.is_contiguous()):
+        raise ValueError("key_src/value_src must be contiguous [T, KV, D]")
+    if block_ids.dtype != torch.int64 or token_offsets.dtype != torch.int64:
+        raise ValueError("block_ids and token_offsets must be int64")
+    t, kv, d = key_src.shape
+    _lib.call("vaa_write_kv_batch", key_dst.data_ptr(), value_dst.data_ptr(), key_src.data_ptr(),
+              value_src.data_ptr(), block_ids.data_ptr(), token_offsets.data_ptr(), t, kv, d,
+              stride_block, stride_head, stride_token, num_blocks, _lib.stream_handle(stream))
+
+
+def write_kv_single(key_dst: torch.Tensor, value_dst: torch.Tensor, key_src: torch.Tensor,
+                    value_src: torch.Tensor, block_id: int, token_offset: int,
+                    stride_block: int, stride_head: int, stride_token: int,
+                    num_blocks: int, stream=None) -> None:
+    """Device counterpart of metal_write_kv_single (kv_write.c:84-107)."""
+    _require_gpu(key_dst, value_dst, key_src, value_src)
+    kv, d = key_src.shape[-2:]
+    _lib.call("vaa_write_kv_single", key_dst.data_ptr(), value_dst.data_ptr(), key_src.data_ptr(),
+              value_src.data_ptr(), int(block_id), int(token_offset), kv, d, stride_block,
+              stride_head, stride_token, num_blocks, _lib.stream_handle(stream))
+
+
+# ----------------------------------------------------------------- attention
+
+
+def _check_tables(block_table: torch.Tensor, seq_lens: torch.Tensor) -> None:
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
+        raise ValueError("block_table must be a contiguous int32 [num_seqs, max_blocks] tensor")
+    if seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous():
+        raise ValueError("seq_lens must be a contiguous int32 tensor")
+    if block_table.shape[0] < seq_lens.numel():
+        raise ValueError("block_table has fewer rows than seq_lens")
+
+
+_workspaces: dict[int, torch.Tensor] = {}
+_counters: dict[int, torch.Tensor] = {}
+
+
+def _dev_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def decode_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Grow-only split-K scratch (partials) per device, reused across calls."""
+    idx = _dev_index(device)
+    ws = _workspaces.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[idx] = ws
+    return ws
+
+
+def decode_counters(count: int, device: torch.device) -> torch.Tensor:
+    """Grow-only int32 counters per device, zero-filled once when allocated.
+
+    Each completed decode call leaves the counters it used at zero, so the
+    buffer stays valid for every later shape.  Calls sharing it are ordered on
+    torch's current stream.
+    """
+    idx = _dev_index(device)
+    c = _counters.get(idx)
+    if c is None or c.numel() < count:
+        c = torch.zeros(max(count, 4096), dtype=torch.int32, device=device)
+        _counters[idx] = c
+    return c
+
+
+def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
+    part = ctypes.c_int32(0)
+    n = _lib.load().vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part))
+    return int(n), int(part.value)
+
+
+def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                 block_table: torch.Tensor, seq_lens: torch.Tensor, *, scale: float,
+                 max_seq_len: int, layout: str = "kernel", output: torch.Tensor | None = None,
+                 new_keys: torch.Tensor | None = None, new_values: torch.Tensor | None = None,
+                 partition_size: int = 0, workspace: torch.Tensor | None = None,
+                 counters: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Paged GQA decode attention, one query token per sequence.
+
+    query [num_seqs, H, D] fp16; returns/fills output [num_seqs, H, D].  With
+    new_keys/new_values ([num_seqs, KV, D]) the token at position
+    seq_lens[s]-1 is written to the cache by the same launch (fused KV write).
+    max_seq_len must bound seq_lens (it sizes the split-K grid).
+    """
+    _require_gpu(query, key_cache, value_cache, block_table, seq_lens, output, new_keys, new_values)
+    _require_dtype(query, torch.float16, "query")
+    _check_tables(block_table, seq_lens)
+    num_seqs = seq_lens.numel()
+    if output is None:
+        output = torch.empty(query.shape, dtype=torch.float16, device=query.device)
+    if query.shape[0] < num_seqs or output.shape[0] < num_seqs:
+        raise ValueError("query/output have fewer rows than sequences")
+    if (new_keys is None) != (new_values is None):
+        raise ValueError("new_keys and new_values go together")
+    if new_keys is not None and new_keys.stride() != new_values.stride():
+        raise ValueError("new_keys and new_values must share strides")
+    p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
+                    num_query_heads=query.shape[1], scale=scale, num_seqs=num_seqs,
+                    max_seq_len=max_seq_len, max_blocks_per_seq=block_table.shape[1],
+                    query=query, output=output, new_kv=new_keys, partition_size=partition_size)
+    if query.shape[2] != p.head_size:
+        raise ValueError(f"query head_size {query.shape[2]} != cache head_size {p.head_size}")
+    nbytes, _ = decode_workspace_size(p)
+    ws_ptr, ws_len, cnt_ptr = None, 0, None
+    if nbytes:
+        if workspace is None:
+            workspace = decode_workspace(nbytes, query.device)
+        if workspace.numel() * workspace.element_size() < nbytes:
+            raise ValueError(f"workspace smaller than {nbytes} bytes")
+        ncnt = num_seqs * p.num_kv_heads
+        if counters is None:
+            counters = decode_counters(ncnt, query.device)
+        if counters.dtype != torch.int32 or counters.numel() < ncnt:
+            raise ValueError(f"counters must be int32 with >= {ncnt} zeroed entries")
+        ws_ptr, ws_len = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        cnt_ptr = counters.data_ptr()
+    _lib.call("vaa_paged_attention_decode", ctypes.byref(p), query.data_ptr(),
+              key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+              seq_lens.data_ptr(), output.data_ptr(), _ptr(new_keys), _ptr(new_values),
+              ws_ptr, ws_len, cnt_ptr, _lib.stream_handle(stream))
+    return output
+
+
+def paged_prefill(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                  block_table: torch.Tensor, token_to_seq: torch.Tensor,
+                  positions: torch.Tensor, *, scale: float, layout: str = "kernel",
+                  output: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Chunked-prefill attention: token t attends to cache positions [0, positions[t]].
+
+    query [num_tokens, H, D] fp16; the tokens' own K/V must already be cached.
+    Rows the reference kernel leaves unwritten (invalid sequence, negative
+    position, context past the block table, invalid block) stay untouched.
+    """
+    _require_gpu(query, key_cache, value_cache, block_table, token_to_seq, positions, output)
+    _require_dtype(query, torch.float16, "query")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
+        raise ValueError("block_table must be a contiguous int32 2-D tensor")
+    for t, n in ((token_to_seq, "token_to_seq"), (positions, "positions")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous int32 tensor")
+    num_tokens = query.shape[0]
+    if token_to_seq.numel() < num_tokens or positions.numel() < num_tokens:
+        raise ValueError("token_to_seq/positions shorter than query")
+    if output is None:
+        output = torch.zeros(query.shape, dtype=torch.float16, device=query.device)
+    p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
+                    num_query_heads=query.shape[1], scale=scale, num_seqs=block_table.shape[0],
+                    max_blocks_per_seq=block_table.shape[1], query=query, output=output)
+    _lib.call("vaa_paged_attention_prefill", ctypes.byref(p), query.data_ptr(),
+              key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+              token_to_seq.data_ptr(), positions.data_ptr(), output.data_ptr(), num_tokens,
+              _lib.stream_handle(stream))
+    return output
+
+
+def build_token_index(query_start_loc: torch.Tensor, seq_lens: torch.Tensor, num_tokens: int,
+                      stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(token_to_seq, positions) int32 [num_tokens] computed on the device."""
+    _require_gpu(query_start_loc, seq_lens)
+    for t, n in ((query_start_loc, "query_start_loc"), (seq_lens, "seq_lens")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous int32 tensor")
+    num_seqs = query_start_loc.numel() - 1
+    if num_seqs < 0 or seq_lens.numel() < num_seqs:
+        raise ValueError("query_start_loc must have num_seqs + 1 entries")
+    tok = torch.empty(num_tokens, dtype=torch.int32, device=query_start_loc.device)
+    pos = torch.empty(num_tokens, dtype=torch.int32, device=query_start_loc.device)
+    _lib.call("vaa_build_token_index", query_start_loc.data_ptr(), seq_lens.data_ptr(), num_seqs,
+              num_tokens, tok.data_ptr(), pos.data_ptr(), _lib.stream_handle(stream))
+    return tok, pos
+
+
+def build_slot_mapping(block_table: torch.Tensor, block_size: int, token_to_seq: torch.Tensor,
+                       positions: torch.Tensor, stream=None) -> torch.Tensor:
+    """int64 slot_mapping for (token_to_seq, positions) through block_table."""
+    _require_gpu(block_table, token_to_seq, positions)
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
+        raise ValueError("block_table must be a contiguous int32 2-D tensor")
+    n = token_to_seq.numel()
+    out = torch.empty(n, dtype=torch.int64, device=token_to_seq.device)
+    _lib.call("vaa_build_slot_mapping", block_table.data_ptr(), block_table.shape[1], block_size,
+              token_to_seq.data_ptr(), positions.data_ptr(), block_table.shape[0], n,
+              out.data_ptr(), _lib.stream_handle(stream))
+    return out
+
+
+# ----------------------------------------------------------------- layer ops
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *,
+             residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+             stream=None) -> torch.Tensor:
+    """half(x * rsqrt(mean(x^2) + eps) * w) [+ residual], rows of a 2-D view."""
+    _require_gpu(x, weight, residual, out)
+    _require_dtype(x, torch.float16, "x")
+    _require_dtype(weight, torch.float16, "weight")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be [num_tokens, hidden] with contiguous rows")
+    t, h = x.shape
+    if weight.numel() != h or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [hidden] tensor")
+    if out is None:
+        out = torch.empty_like(x)
+    for r, n in ((out, "out"), (residual, "residual")):
+        if r is not None and (r.shape != x.shape or r.stride(1) != 1 or r.dtype != torch.float16):
+            raise ValueError(f"{n} must match x ([T, H] fp16, contiguous rows)")
+    _lib.call("vaa_rmsnorm", x.data_ptr(), out.data_ptr(), weight.data_ptr(), _ptr(residual), t, h,
+              x.stride(0), out.stride(0), residual.stride(0) if residual is not None else 0,
+              float(eps), _lib.stream_handle(stream))
+    return out
+
+
+def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float,
+                       device: torch.device | str = "cuda") -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos/sin tables [max_position, rotary_dim // 2].
+
+    Same construction as EngineRoPE._precompute_cache (elementwise.py:680-697):
+    float32 numpy, inv_freq = 1 / base ** (arange(half) / half).
+    """
+    import numpy as np
+
+    half = rotary_dim // 2
+    inv_freq = 1.0 / (base ** (np.arange(0, half, dtype=np.float32) / half))
+    positions = np.arange(max_position, dtype=np.float32)
+    freqs = np.outer(positions, inv_freq)
+    cos = torch.from_numpy(np.cos(freqs).astype(np.float32))
+    sin = torch.from_numpy(np.sin(freqs).astype(np.float32))
+    return cos.to(device), sin.to(device)
+
+
+def rope_neox_(query: torch.Tensor, key: torch.Tensor | None, cos_cache: torch.Tensor,
+               sin_cache: torch.Tensor, positions: torch.Tensor, *,
+               rotary_dim: int | None = None, stream=None) -> None:
+    """In-place NeoX rotation of query [T, H, D] and key [T, KV, D]."""
+    _require_gpu(query, key, cos_cache, sin_cache, positions)
+    _require_dtype(query, torch.float16, "query")
+    if query.dim() != 3 or query.stride(2) != 1 or query.stride(1) != query.shape[2]:
+        raise ValueError("query must be [T, H, D] with heads packed at stride D")
+    if key is not None and (key.dim() != 3 or key.stride(2) != 1 or key.stride(1) != key.shape[2]
+                            or key.dtype != torch.float16 or key.shape[0] != query.shape[0]):
+        raise ValueError("key must be fp16 [T, KV, D] with heads packed at stride D")
+    if positions.dtype != torch.int32 or not positions.is_contiguous():
+        raise ValueError("positions must be a contiguous int32 tensor")
+    t, h, d = query.shape
+    rot = rotary_dim or d
+    if cos_cache.dtype != torch.float32 or cos_cache.dim() != 2 or cos_cache.shape[1] != rot // 2:
+        raise ValueError("cos/sin caches must be fp32 [max_position, rotary_dim/2]")
+    if not (cos_cache.is_contiguous() and sin_cache.is_contiguous()):
+        raise ValueError("cos/sin caches must be contiguous")
+    kv = key.shape[1] if key is not None else 0
+    _lib.call("vaa_rope_neox", query.data_ptr(), _ptr(key), cos_cache.data_ptr(),
+              sin_cache.data_ptr(), positions.data_ptr(), t, h, kv, d, rot, query.stride(0),
+              key.stride(0) if key is not None else 0, cos_cache.shape[0],
+              _lib.stream_handle(stream))
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
+             stream=None) -> torch.Tensor:
+    """out = half(silu(float(gate)) * float(up)); 1-D or row-strided 2-D views."""
+    _require_gpu(gate, up, out)
+    for t, n in ((gate, "gate"), (up, "up")):
+        _require_dtype(t, torch.float16, n)
+    if gate.shape != up.shape:
+        raise ValueError("gate and up must have the same shape")
+    if out is None:
+        out = torch.empty(gate.shape, dtype=torch.float16, device=gate.device)
+    if out.shape != gate.shape or out.dtype != torch.float16:
+        raise ValueError("out must match gate")
+    if gate.is_contiguous() and up.is_contiguous() and out.is_contiguous():
+        _lib.call("vaa_silu_mul", gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                  _lib.stream_handle(stream))
+        return out
+    if gate.dim() != 2:
+        raise ValueError("non-contiguous gate/up/out must be 2-D row-strided views")
+    g2, u2, o2 = gate, up, out
+    for x in (g2, u2, o2):
+        if x.stride(-1) != 1:
+            raise ValueError("last dimension must be contiguous")
+    _lib.call("vaa_silu_mul_2d", g2.data_ptr(), u2.data_ptr(), o2.data_ptr(), g2.shape[0],
+              g2.shape[1], g2.stride(0), u2.stride(0), o2.stride(0), _lib.stream_handle(stream))
+    return out
+
+
+def default_scale(head_size: int) -> float:
+    return 1.0 / math.sqrt(head_size)
