@@ -161,15 +161,10 @@ size_t vaa_paged_attention_decode_workspace_size(const vaa_attn_params* p,
  * new_values are non-null the token at position L-1 is taken from them and
  * written to the cache in the same launch (the fused KV write); when they are
  * null the cache must already hold it.  Long contexts are split into
- * partitions whose partial (max, sum, acc) are merged (log-sum-exp) by the
- * last partition to finish, inside the same launch.  When split-K is used
- * (workspace size > 0) the workspace must hold
- * vaa_paged_attention_decode_workspace_size(p) bytes of scratch, and
- * `counters` must point to num_seqs * num_kv_heads int32 that are zero before
- * the call; every completed call leaves them zero, so one zero fill at
- * allocation suffices.  The counters must be dedicated to this use and not
- * shared by calls that can run concurrently.  Both may be null when every
- * sequence fits one partition.
+ * partitions whose partial (max, sum, acc) go to the workspace and are merged
+ * (log-sum-exp) by a second kernel on the same stream; the workspace must hold
+ * vaa_paged_attention_decode_workspace_size(p) bytes (it may be null when that
+ * size is 0) and must not be shared by calls that can run concurrently.
  */
 int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
                                uint16_t* key_cache, uint16_t* value_cache,
@@ -177,8 +172,7 @@ int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
                                const int32_t* seq_lens, uint16_t* output,
                                const uint16_t* new_keys,
                                const uint16_t* new_values, void* workspace,
-                               size_t workspace_bytes, int32_t* counters,
-                               void* stream);
+                               size_t workspace_bytes, void* stream);
 
 /*
  * Chunked-prefill paged attention (MFMA).  Replaces paged_attention_v2_prefill

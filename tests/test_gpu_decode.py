@@ -50,7 +50,7 @@ def _run(kc, vc, bt, lens, q, nk, nv, *, layout="kernel", fused=True, part=0, sc
     return out, ref, kd, vd, kc_ref, vc_ref
 
 
-@pytest.mark.parametrize("part", [0, 64, 128, 512])
+@pytest.mark.parametrize("part", [0, 128, 256, 512])
 def test_decode_c1_shape(gpu, part):
     """C1 shape (14q/2kv, D64, GQA 7), fused write, several partition sizes."""
     lens = [37, 512, 16, 201]
@@ -85,6 +85,26 @@ def test_decode_head_shapes(gpu, D, H, KV):
     assert_close(host(out), ref, what=f"decode D={D} H={H} KV={KV}")
 
 
+@pytest.mark.parametrize("bs", [32, 64])
+def test_decode_larger_block_size(gpu, bs):
+    """block_size a multiple of 16 (tiles of 16 tokens inside larger blocks)."""
+    lens = [1, 31, 33, 2000, 5000, 700]
+    kc, vc, bt, L, q, nk, nv = _case(6, 32, 8, 128, lens, bs=bs, seed=13)
+    for part in (0, 128, 1024):
+        out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=part)
+        assert_close(host(out), ref, what=f"decode bs={bs} part={part}")
+        assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
+
+
+def test_decode_long_contexts_many_windows(gpu):
+    """Runs longer than one 64-block window per wave (C4-like lengths)."""
+    lens = [32768, 20000, 4096, 9999]
+    kc, vc, bt, L, q, nk, nv = _case(4, 32, 8, 128, lens, seed=14)
+    for part in (0, 8192, 32768):
+        out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=part)
+        assert_close(host(out), ref, what=f"decode long part={part}")
+
+
 def test_decode_unfused_reads_cache(gpu):
     lens = [100, 2000, 33]
     kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, lens, seed=4)
@@ -112,9 +132,9 @@ def test_decode_zero_and_edge_lengths(gpu):
 def test_decode_split_matches_unsplit(gpu):
     lens = [5000, 3000, 7777]
     kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, lens, seed=7)
-    a, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=64)
+    a, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=128)
     b, *_ = _run(kc, vc, bt, L, q, nk, nv, part=8192)
-    assert_close(host(a), ref, what="split 64")
+    assert_close(host(a), ref, what="split 128")
     assert_close(host(b), ref, what="split 8192")
     assert_close(host(a), host(b).astype(np.float64), what="split vs unsplit")
 

@@ -7,13 +7,18 @@
 // zero row for seq_len <= 0).
 //
 // Work decomposition
-//   grid  = (partition, kv_head, seq); one workgroup serves every query head
-//           of the GQA group, so each K/V byte is read from HBM once.
-//   block = 4 waves; the partition's 16-token tiles are split between them and
-//           each wave keeps its own (max, sum, acc) until a final LDS combine.
-//   split-K = partitions of 512 tokens by default; partials (max, sum, acc) go
-//           to the workspace and the last partition of a (seq, kv_head) to
-//           finish merges them (log-sum-exp) in the same launch.
+//   grid     = (partition, kv_head, seq); one workgroup serves every query
+//              head of the GQA group, so each K/V byte is read from HBM once.
+//   block    = 8 waves; each wave streams a contiguous run of 16-token tiles
+//              with its own (max, sum, acc) and the waves are combined in LDS
+//              at the end.
+//   split-K  = only when the (seq, kv_head) pairs cannot fill the GPU or the
+//              lengths are unequal; partials (max, sum, acc) go to a workspace
+//              and a second kernel merges them (log-sum-exp).  The merge is a
+//              separate launch on purpose: a cross-workgroup handoff inside
+//              one launch needs agent-scope release/acquire (an L2 writeback
+//              and invalidate per workgroup on every XCD), which measured 3x
+//              slower than the kernel boundary.
 //
 // Per 16-token tile a wave does
 //   S^T[16 tok x 16 heads] = K[16 x D] * Q^T[D x 16]   (D/32 x mfma 16x16x32)
@@ -28,14 +33,17 @@
 // Memory: each lane loads 16-byte pieces of one K row straight into the MFMA
 // A-operand registers (the contraction index d is permuted identically in K
 // and Q).  V is loaded with fully coalesced 16-byte loads, stored to a per-wave
-// LDS tile (XOR-swizzled 16-byte chunks) and read back transposed.
+// LDS tile (XOR-swizzled 16-byte chunks) and read back transposed.  Loads run
+// two tiles ahead of the math in a rotated three-buffer pipeline, and the
+// wave's block-table entries sit in a VGPR (one per lane) read with readlane,
+// so the steady-state loop issues no scalar memory loads.
 #include "common.h"
 
 namespace vaa {
 namespace {
 
-constexpr int kDecodeWaves = 4;
-constexpr int kTile = 16;  // tokens per MFMA tile
+constexpr int kWaves = 8;   // waves per workgroup
+constexpr int kTile = 16;   // tokens per MFMA tile
 
 struct DecodeArgs {
   const f16* q;
@@ -48,8 +56,6 @@ struct DecodeArgs {
   const f16* new_v;
   float* ws_acc;  // [seq][qhead][part][D] unnormalised partial outputs
   float* ws_ml;   // [seq][qhead][part][2] (max in log2 domain, sum)
-  int* ws_cnt;    // [seq][kv_head] finished-partition counters (zero between calls)
-                  // (a dedicated caller buffer, never part of the partials)
   float scale_log2;
   int num_seqs, max_blocks, block_size, num_kv_heads, num_q_heads, G;
   int part_tiles, max_parts;
@@ -60,9 +66,9 @@ struct DecodeArgs {
 
 template <int D>
 struct Cfg {
-  static constexpr int NS = D / 32;       // QK mfma count (K-dim 32)
-  static constexpr int NDT = D / 16;      // PV mfma count (16 output dims each)
-  static constexpr int CH = D / 8;        // 16-byte chunks per row
+  static constexpr int NS = D / 32;               // QK mfma count (K-dim 32)
+  static constexpr int NDT = D / 16;              // PV mfma count (16 dims each)
+  static constexpr int CH = D / 8;                // 16-byte chunks per row
   static constexpr int VLD = kTile * CH / kWave;  // V loads per lane per tile
   static constexpr bool SWZ = (CH == 8 || CH == 16);
 };
@@ -74,59 +80,109 @@ __device__ __forceinline__ int swz(int row) {
 }
 
 template <int D>
-struct TileRegs {
+struct Tile {
   u32x4 k[Cfg<D>::NS];
   u32x4 v[Cfg<D>::VLD];
-  int vsti;  // index of the V chunk holding the new token (fused write), or -1
 };
 
-// Issue the loads of tile j (16 tokens) for this lane.  valid_rows is the
-// number of real tokens in the tile (0 for an invalid block).
+// Per-lane constants of the tile loads and LDS traffic.
 template <int D>
-__device__ __forceinline__ void load_tile(const DecodeArgs& a, int seq, int kvh,
-                                          int L, int j, int lane, int new_row,
-                                          TileRegs<D>& r, int& valid_rows,
-                                          f16*& kst, f16*& vst) {
-  const int tok0 = j * kTile;
-  const int bi = tok0 / a.block_size;
-  const int row0 = tok0 - bi * a.block_size;
-  int64_t phys = a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi];
-  valid_rows = min(kTile, L - tok0);
-  if (phys < 0 || phys >= a.num_blocks) {
-    phys = 0;
-    valid_rows = 0;
-  }
-  const f16* kb = a.kc + phys * a.k_sb + kvh * a.k_sh + row0 * a.k_st;
-  const f16* vb = a.vc + phys * a.v_sb + kvh * a.v_sh + row0 * a.v_st;
-  const int c16 = lane & 15, g = lane >> 4;
-  // K: row c16, NS contiguous 16-byte pieces starting at element g*D/4.
-  const f16* kp = kb + c16 * a.k_st + g * (D / 4);
-  kst = nullptr;
-  if (c16 == new_row && valid_rows > 0) {
-    kst = const_cast<f16*>(kp);
-    kp = a.new_k + seq * a.n_st + kvh * a.n_sh + g * (D / 4);
-  }
+struct LaneMap {
+  uint32_t koff;               // element offset of this lane's K piece in a tile
+  uint32_t voff[Cfg<D>::VLD];  // element offset of V chunk i in a tile
+  int vrow[Cfg<D>::VLD];       // tile row of V chunk i
+  uint32_t wlds[Cfg<D>::VLD];  // LDS element offset where V chunk i is stored
+  uint32_t rbase[4];           // LDS row base of V^T reads, r = 0..3
+  int rsw[4];                  // chunk swizzle of those rows
+};
+
+// Block-table window: lane i of `vals` holds the entry of block blk0 + i, so a
+// chunk of up to 64 tiles (block_size 16) reads its physical blocks with
+// readlane and the pipelined loop issues no scalar or table loads.
+__device__ __forceinline__ int load_window(const DecodeArgs& a, int seq, int blk0, int lane) {
+  const int e = blk0 + lane;
+  return e < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + e] : -1;
+}
+
+__device__ __forceinline__ int64_t window_block(const DecodeArgs& a, int vals, int blk0,
+                                                int j) {
+  return __builtin_amdgcn_readlane(vals, (j * kTile) / a.block_size - blk0);
+}
+
+template <int D>
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
+                                          int64_t vbase, const LaneMap<D>& m,
+                                          int64_t phys, int j, Tile<D>& t) {
+  const int row0 = (j * kTile) % a.block_size;
+  if (phys < 0 || phys >= a.num_blocks) phys = 0;  // masked by the caller
+  const f16* kb = a.kc + kbase + phys * a.k_sb + row0 * a.k_st;
+  const f16* vb = a.vc + vbase + phys * a.v_sb + row0 * a.v_st;
 #pragma unroll
-  for (int s = 0; s < Cfg<D>::NS; ++s) r.k[s] = ld16(kp + 8 * s);
-  // V: coalesced; flat chunk f = i*64 + lane -> (row f/CH, chunk f%CH).
-  vst = nullptr;
-  r.vsti = -1;
+  for (int s = 0; s < Cfg<D>::NS; ++s) t.k[s] = ld16(kb + m.koff + 8 * s);
 #pragma unroll
-  for (int i = 0; i < Cfg<D>::VLD; ++i) {
-    const int f = i * kWave + lane;
-    const int row = f / Cfg<D>::CH, ch = f % Cfg<D>::CH;
-    const f16* vp = vb + row * a.v_st + ch * 8;
-    if (row == new_row && valid_rows > 0) {
-      vst = const_cast<f16*>(vp);  // cache slot of this chunk
-      r.vsti = i;
-      vp = a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8;
-    }
-    r.v[i] = ld16(vp);
+  for (int i = 0; i < Cfg<D>::VLD; ++i) t.v[i] = ld16(vb + m.voff[i]);
+}
+
+// One tile of math.  valid = number of real tokens in the tile (16 for every
+// tile but the sequence's last one; 0 for an invalid block).
+template <int D>
+__device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
+                                          const u32x4* qb, f16* vt, int valid, int g,
+                                          float scale_log2, float& m_run, float& l_part,
+                                          f32x4* acc) {
+  using C = Cfg<D>;
+  // V tile -> LDS; rows past the sequence end are zeroed so stale cache
+  // contents (even NaN) can never reach the accumulators.
+#pragma unroll
+  for (int i = 0; i < C::VLD; ++i) {
+    const u32x4 v = m.vrow[i] < valid ? t.v[i] : u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(vt + m.wlds[i]) = v;
+  }
+  // S^T = K Q^T.
+  f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) {
+    s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, t.k[s]),
+                                                __builtin_bit_cast(f16x8, qb[s]), s4,
+                                                0, 0, 0);
+  }
+  // Online softmax in the log2 domain; lane = head, tokens 4g..4g+3.
+  float x[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    x[r] = (4 * g + r < valid) ? s4[r] * scale_log2 : -INFINITY;
+    mx = fmaxf(mx, x[r]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  const float m_new = fmaxf(m_run, mx);
+  if (m_new != m_run) {  // the running max moved: rescale (rare after warm-up)
+    const float alpha = fast_exp2(m_run - m_new);  // 0 when m_run = -inf
+    l_part *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
+    m_run = m_new;
+  }
+  const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
+  f16x4 ph;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    ph[r] = f2h(fast_exp2(x[r] - m_sub));
+    l_part += h2f(ph[r]);
+  }
+  // O^T += V^T P^T; lane reads V[4g+r][16dt + c16] from LDS.
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) {
+    f16x4 va;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) va[r] = vt[m.rbase[r] + (((2 * dt) ^ m.rsw[r]) << 3)];
+    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc[dt], 0, 0, 0);
   }
 }
 
 template <int D>
-__global__ void __launch_bounds__(kDecodeWaves* kWave)
+__global__ void __launch_bounds__(kWaves* kWave)
 paged_decode_kernel(DecodeArgs a) {
   using C = Cfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -154,13 +210,33 @@ paged_decode_kernel(DecodeArgs a) {
   if (part >= n_parts) return;
   const int t0 = part * a.part_tiles;
   const int t1 = (part == a.max_parts - 1) ? n_tiles : min(t0 + a.part_tiles, n_tiles);
-  const int per = (t1 - t0 + kDecodeWaves - 1) / kDecodeWaves;
+  const int per = (t1 - t0 + kWaves - 1) / kWaves;
   const int jb = t0 + wave * per;
   const int je = min(jb + per, t1);
 
-  // Row of the new token inside the last tile (fused KV write), else -1.
-  int new_row_last = -1;
-  if (a.new_k != nullptr && Lorig == L) new_row_last = (L - 1) - (n_tiles - 1) * kTile;
+  // The sequence's last tile is peeled when it is partial or holds the new
+  // token (fused KV write); every other tile is full and runs the pipeline.
+  const bool fused = a.new_k != nullptr && Lorig == L;
+  const int special = (fused || (L % kTile) != 0) ? n_tiles - 1 : n_tiles;
+  const int jm = min(je, special);
+
+  LaneMap<D> m;
+  m.koff = c16 * static_cast<uint32_t>(a.k_st) + g * (D / 4);
+#pragma unroll
+  for (int i = 0; i < C::VLD; ++i) {
+    const int f = i * kWave + lane;
+    const int row = f / C::CH, ch = f % C::CH;
+    m.vrow[i] = row;
+    m.voff[i] = row * static_cast<uint32_t>(a.v_st) + ch * 8;
+    m.wlds[i] = row * D + ((ch ^ swz<D>(row)) * 8);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * g + r;
+    m.rsw[r] = swz<D>(row);
+    m.rbase[r] = row * D + (c16 & 7) + ((c16 >> 3) << 3);
+  }
+  const int64_t kbase = kvh * a.k_sh, vbase = kvh * a.v_sh;
 
   // Q^T as the B operand: lane holds Q[head c16][g*D/4 + 8s .. +7].
   u32x4 qb[C::NS];
@@ -168,9 +244,7 @@ paged_decode_kernel(DecodeArgs a) {
     const bool hv = c16 < G;
     const f16* qp = a.q + seq * a.q_st + (kvh * G + (hv ? c16 : 0)) * a.q_sh + g * (D / 4);
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) {
-      qb[s] = hv ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int s = 0; s < C::NS; ++s) qb[s] = hv ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
   f16* vt = reinterpret_cast<f16*>(smem) + wave * (kTile * D);
@@ -179,106 +253,90 @@ paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (jb < je) {
-    TileRegs<D> cur;
-    int cur_valid;
-    f16 *cur_kst, *cur_vst;
-    load_tile<D>(a, seq, kvh, L, jb, lane, jb == n_tiles - 1 ? new_row_last : -1,
-                 cur, cur_valid, cur_kst, cur_vst);
-    for (int j = jb; j < je; ++j) {
-      TileRegs<D> nxt;
-      int nxt_valid = 0;
-      f16 *nxt_kst = nullptr, *nxt_vst = nullptr;
-      if (j + 1 < je)
-        load_tile<D>(a, seq, kvh, L, j + 1, lane,
-                     j + 1 == n_tiles - 1 ? new_row_last : -1, nxt, nxt_valid,
-                     nxt_kst, nxt_vst);
-
-      // Fused KV write: the lanes that hold the new token store it.
-      if (cur_kst) {
-#pragma unroll
-        for (int s = 0; s < C::NS; ++s) st16(cur_kst + 8 * s, cur.k[s]);
-      }
-      if (cur_vst) {
-#pragma unroll
-        for (int i = 0; i < C::VLD; ++i)
-          if (i == cur.vsti) st16(cur_vst, cur.v[i]);
-      }
-
-      // V tile -> LDS (rows past the sequence end are zeroed so stale cache
-      // contents can never reach the accumulators).
-#pragma unroll
-      for (int i = 0; i < C::VLD; ++i) {
-        const int f = i * kWave + lane;
-        const int row = f / C::CH, ch = f % C::CH;
-        u32x4 v = row < cur_valid ? cur.v[i] : u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(vt + row * D + ((ch ^ swz<D>(row)) * 8)) = v;
-      }
-
-      // S^T = K Q^T.
-      f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < C::NS; ++s) {
-        s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(f16x8, cur.k[s]), __builtin_bit_cast(f16x8, qb[s]),
-            s4, 0, 0, 0);
-      }
-      // Online softmax (log2 domain); lane = head c16, tokens 4g..4g+3.
-      float x[4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = (4 * g + r < cur_valid) ? s4[r] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, x[r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
-      const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;
-      f16x4 ph;
-      float psum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ph[r] = f2h(fast_exp2(x[r] - m_sub));
-        psum += h2f(ph[r]);
-      }
-      l_part = l_part * alpha + psum;
-      m_run = m_new;
-      if (alpha != 1.f) {
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
-      }
-
-      // O^T += V^T P^T; lane reads V[4g+r][16dt + c16] from LDS.
-#pragma unroll
-      for (int dt = 0; dt < C::NDT; ++dt) {
-        const int d = 16 * dt + c16;
-        f16x4 va;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 4 * g + r;
-          va[r] = vt[row * D + (((d >> 3) ^ swz<D>(row)) * 8) + (d & 7)];
-        }
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc[dt], 0, 0, 0);
-      }
-
-      cur = nxt;
-      cur_valid = nxt_valid;
-      cur_kst = nxt_kst;
-      cur_vst = nxt_vst;
+  auto valid_of = [&](int64_t p) { return (p < 0 || p >= a.num_blocks) ? 0 : kTile; };
+  // Each chunk covers the tiles of 64 consecutive blocks (one VGPR of
+  // block-table entries).
+  for (int cb = jb; cb < jm;) {
+    const int blk0 = (cb * kTile) / a.block_size;
+    const int ce = min(jm, ((blk0 + kWave) * a.block_size) / kTile);
+    const int vals = load_window(a, seq, blk0, lane);
+    // Three rotating tile buffers; loads run two tiles ahead.  Prefetch
+    // indices past the chunk are clamped to its last tile (an L2 hit), which
+    // keeps the loop free of branches around loads.
+    const int jl = ce - 1;
+    Tile<D> r0, r1, r2;
+    int64_t p0 = window_block(a, vals, blk0, cb);
+    issue_tile<D>(a, kbase, vbase, m, p0, cb, r0);
+    int64_t p1 = window_block(a, vals, blk0, min(cb + 1, jl));
+    issue_tile<D>(a, kbase, vbase, m, p1, min(cb + 1, jl), r1);
+    int64_t p2;
+    int j = cb;
+    for (; j + 3 <= ce; j += 3) {
+      p2 = window_block(a, vals, blk0, min(j + 2, jl));
+      issue_tile<D>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
+      tile_math<D>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
+      p0 = window_block(a, vals, blk0, min(j + 3, jl));
+      issue_tile<D>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
+      tile_math<D>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
+      p1 = window_block(a, vals, blk0, min(j + 4, jl));
+      issue_tile<D>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
+      tile_math<D>(m, r2, qb, vt, valid_of(p2), g, a.scale_log2, m_run, l_part, acc);
     }
+    // Remainder (0..2 tiles): r0 holds tile j, r1 tile j+1.
+    if (j < ce) {
+      tile_math<D>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
+      if (j + 1 < ce)
+        tile_math<D>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
+    }
+    cb = ce;
+  }
+
+  // Peeled last tile: partial and/or carrying the new token, which is read
+  // from new_k/new_v and written to the cache here (the fused KV write).
+  if (special >= jb && special < je) {
+    const int j = special;
+    const int tok0 = j * kTile;
+    const int bi = tok0 / a.block_size;
+    int64_t phys = bi < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi] : -1;
+    const bool bvalid = phys >= 0 && phys < a.num_blocks;
+    const int valid = bvalid ? min(kTile, L - tok0) : 0;
+    if (!bvalid) phys = 0;
+    const int new_row = fused ? (L - 1) - tok0 : -1;
+    const int row0 = tok0 % a.block_size;
+    f16* kb = a.kc + kbase + phys * a.k_sb + row0 * a.k_st;
+    f16* vb = a.vc + vbase + phys * a.v_sb + row0 * a.v_st;
+    Tile<D> t;
+    {
+      const bool mine = (c16 == new_row) && bvalid;
+      const f16* kp = mine ? a.new_k + seq * a.n_st + kvh * a.n_sh + g * (D / 4)
+                           : kb + m.koff;
+#pragma unroll
+      for (int s = 0; s < C::NS; ++s) t.k[s] = ld16(kp + 8 * s);
+      if (mine) {
+#pragma unroll
+        for (int s = 0; s < C::NS; ++s) st16(kb + m.koff + 8 * s, t.k[s]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::VLD; ++i) {
+      const bool mine = (m.vrow[i] == new_row) && bvalid;
+      const int ch = (i * kWave + lane) % C::CH;
+      const f16* vp = mine ? a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8 : vb + m.voff[i];
+      t.v[i] = ld16(vp);
+      if (mine) st16(vb + m.voff[i], t.v[i]);
+    }
+    tile_math<D>(m, t, qb, vt, valid, g, a.scale_log2, m_run, l_part, acc);
   }
 
   // Sum over the four token groups of this head.
   l_part += __shfl_xor(l_part, 16, kWave);
   l_part += __shfl_xor(l_part, 32, kWave);
 
-  // Cross-wave combine through LDS: wm/wl [wave][G], wa [wave][G][D].
+  // Cross-wave combine through LDS: wm/wl [wave][16], wa [wave][G][D].
   __syncthreads();
   float* wm = reinterpret_cast<float*>(smem);
-  float* wl = wm + kDecodeWaves * 16;
-  float* wa = wl + kDecodeWaves * 16;
+  float* wl = wm + kWaves * 16;
+  float* wa = wl + kWaves * 16;
   if (c16 < G) {
     if (g == 0) {
       wm[wave * 16 + c16] = m_run;
@@ -301,11 +359,11 @@ paged_decode_kernel(DecodeArgs a) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, wm[w * 16 + h]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w * 16 + h]);
     float num = 0.f, den = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kDecodeWaves; ++w) {
+      for (int w = 0; w < kWaves; ++w) {
         const float mw = wm[w * 16 + h];
         if (mw == -INFINITY) continue;
         const float sc = fast_exp2(mw - M);
@@ -325,65 +383,77 @@ paged_decode_kernel(DecodeArgs a) {
       }
     }
   }
-  if (single) return;
-
-  // Split-K merge by the last partition to finish for this (seq, kv_head):
-  // out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.  No workgroup ever
-  // waits: the others simply exit.  Agent-scope fences order the partials
-  // (written on any XCD) before the counter and the counter before the reads.
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int* cnt = a.ws_cnt + static_cast<int64_t>(seq) * a.num_kv_heads + kvh;
-    const int prev = atomicAdd(cnt, 1);
-    s_last = (prev == n_parts - 1);
-    if (s_last) atomicExch(cnt, 0);  // leave the counter at zero for the next call
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int h = idx / D, d = idx % D;
-    const int qh = kvh * G + h;
-    const int64_t row0 = (static_cast<int64_t>(seq) * H + qh) * a.max_parts;
-    float M = -INFINITY;
-    for (int p = 0; p < n_parts; ++p) {
-      if (a.ws_ml[(row0 + p) * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[(row0 + p) * 2]);
-    }
-    float num = 0.f, den = 0.f;
-    if (M != -INFINITY) {
-      for (int p = 0; p < n_parts; ++p) {
-        const float lp = a.ws_ml[(row0 + p) * 2 + 1];
-        if (!(lp > 0.f)) continue;
-        const float sc = fast_exp2(a.ws_ml[(row0 + p) * 2] - M);
-        num += sc * a.ws_acc[(row0 + p) * D + d];
-        den += sc * lp;
-      }
-    }
-    a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
-  }
 }
 
+// Second pass for split sequences:
+//   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p.
+template <int D>
+__global__ void __launch_bounds__(D)
+paged_decode_merge_kernel(DecodeArgs a) {
+  const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+  int L = a.seq_lens[seq];
+  const int cap = a.max_blocks * a.block_size;
+  if (L > cap) L = cap;
+  if (L <= 0) return;  // zero row written by the decode kernel
+  const int part_tok = a.part_tiles * kTile;
+  const int n_parts = min((L + part_tok - 1) / part_tok, a.max_parts);
+  if (n_parts <= 1) return;  // written directly by the decode kernel
+  const int64_t row0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh) * a.max_parts;
+  float M = -INFINITY;
+  for (int p = 0; p < n_parts; ++p) {
+    if (a.ws_ml[(row0 + p) * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[(row0 + p) * 2]);
+  }
+  float num = 0.f, den = 0.f;
+  if (M != -INFINITY) {
+    for (int p = 0; p < n_parts; ++p) {
+      const float lp = a.ws_ml[(row0 + p) * 2 + 1];
+      if (!(lp > 0.f)) continue;
+      const float sc = fast_exp2(a.ws_ml[(row0 + p) * 2] - M);
+      num += sc * a.ws_acc[(row0 + p) * D + d];
+      den += sc * lp;
+    }
+  }
+  a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
+}
+
+int g_num_cus = 0;
+
+int num_cus() {
+  if (g_num_cus > 0) return g_num_cus;
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0)
+    n = 256;
+  g_num_cus = n;
+  return n;
+}
+
+// Automatic partition size from max_seq_len alone (all sequences assumed at
+// the maximum): split only as far as needed for the workgroups to cover every
+// CU once, in multiples of 16 * kWaves tokens.  Callers that know the lengths
+// pass partition_size explicitly.
 int choose_partition(const vaa_attn_params* p, int* part_out, int* max_parts_out) {
   const int64_t cap = static_cast<int64_t>(p->max_blocks_per_seq) * p->block_size;
   int64_t max_len = p->max_seq_len;
   if (max_len > cap) max_len = cap;
   if (max_len < 1) max_len = 1;
-  int part = p->partition_size;
+  const int quantum = kTile * kWaves;
+  int64_t part = p->partition_size;
   if (part > 0) {
-    if (part % (kTile * kDecodeWaves) != 0)
+    if (part % quantum != 0)
       return fail(VAA_ERR_INVALID_ARG,
-                  "partition_size=%d must be a positive multiple of %d", part,
-                  kTile * kDecodeWaves);
+                  "partition_size=%lld must be a positive multiple of %d",
+                  (long long)part, quantum);
   } else {
     const int64_t pairs = static_cast<int64_t>(p->num_seqs) * p->num_kv_heads;
-    part = 512;
-    while (part > kTile * kDecodeWaves &&
-           pairs * ((max_len + part - 1) / part) < 1024)
-      part /= 2;
+    int64_t splits = pairs > 0 ? (num_cus() + pairs - 1) / pairs : 1;
+    if (splits < 1) splits = 1;
+    part = (max_len + splits - 1) / splits;
+    part = (part + quantum - 1) / quantum * quantum;
   }
-  *part_out = part;
+  if (part > (int64_t{1} << 30)) part = int64_t{1} << 30;
+  *part_out = static_cast<int>(part);
   *max_parts_out = static_cast<int>((max_len + part - 1) / part);
   return VAA_OK;
 }
@@ -417,19 +487,26 @@ int check_params(const vaa_attn_params* p, const char* what) {
     if (s < 0 || s % 8 != 0)
       return fail(VAA_ERR_INVALID_ARG,
                   "%s: strides must be non-negative multiples of 8 elements", what);
+  // In-tile lane offsets are 32-bit.
+  if (p->k_stride_token * kTile >= (int64_t{1} << 31) ||
+      p->v_stride_token * kTile >= (int64_t{1} << 31))
+    return fail(VAA_ERR_INVALID_ARG, "%s: token stride too large", what);
   return VAA_OK;
 }
 
 template <int D>
 int launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream) {
-  const size_t lds_tiles = static_cast<size_t>(kDecodeWaves) * kTile * D * sizeof(f16);
+  const size_t lds_tiles = static_cast<size_t>(kWaves) * kTile * D * sizeof(f16);
   const size_t lds_comb =
-      (2 * kDecodeWaves * 16 + static_cast<size_t>(kDecodeWaves) * a.G * D) * sizeof(float);
+      (2 * kWaves * 16 + static_cast<size_t>(kWaves) * a.G * D) * sizeof(float);
   const size_t lds = lds_tiles > lds_comb ? lds_tiles : lds_comb;
   dim3 grid(a.max_parts, a.num_kv_heads, num_seqs);
-  hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kDecodeWaves * kWave), lds,
-                     stream, a);
-  return check_launch("paged_decode_kernel");
+  hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kWaves * kWave), lds, stream, a);
+  int st = check_launch("paged_decode_kernel");
+  if (st || a.max_parts <= 1) return st;
+  hipLaunchKernelGGL(paged_decode_merge_kernel<D>, dim3(a.num_q_heads, num_seqs), dim3(D),
+                     0, stream, a);
+  return check_launch("paged_decode_merge_kernel");
 }
 
 }  // namespace
@@ -459,7 +536,7 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
                                           const uint16_t* new_keys,
                                           const uint16_t* new_values,
                                           void* workspace, size_t workspace_bytes,
-                                          int32_t* counters, void* stream) {
+                                          void* stream) {
   int st = check_params(p, "vaa_paged_attention_decode");
   if (st) return st;
   if (p->num_seqs == 0) return VAA_OK;
@@ -490,20 +567,15 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   a.new_v = reinterpret_cast<const f16*>(new_values);
   a.ws_acc = nullptr;
   a.ws_ml = nullptr;
-  a.ws_cnt = nullptr;
   if (max_parts > 1) {
     const size_t need = vaa_paged_attention_decode_workspace_size(p, nullptr);
     if (!workspace || workspace_bytes < need)
       return fail(VAA_ERR_WORKSPACE,
                   "vaa_paged_attention_decode: workspace %zu bytes < %zu needed",
                   workspace_bytes, need);
-    if (!counters)
-      return fail(VAA_ERR_WORKSPACE,
-                  "vaa_paged_attention_decode: split-K needs the zeroed counters buffer");
     const size_t rows = static_cast<size_t>(p->num_seqs) * p->num_query_heads * max_parts;
     a.ws_acc = static_cast<float*>(workspace);
     a.ws_ml = a.ws_acc + rows * p->head_size;
-    a.ws_cnt = counters;
   }
   a.scale_log2 = p->scale * kLog2e;
   a.num_seqs = p->num_seqs;

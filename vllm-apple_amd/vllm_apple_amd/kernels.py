@@ -198,36 +198,19 @@ def _check_tables(block_table: torch.Tensor, seq_lens: torch.Tensor) -> None:
 
 
 _workspaces: dict[int, torch.Tensor] = {}
-_counters: dict[int, torch.Tensor] = {}
-
-
 def _dev_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def decode_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """Grow-only split-K scratch (partials) per device, reused across calls."""
+    """Grow-only split-K scratch (partials) per device, reused across calls
+    that are ordered on one stream (torch's current stream by default)."""
     idx = _dev_index(device)
     ws = _workspaces.get(idx)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[idx] = ws
     return ws
-
-
-def decode_counters(count: int, device: torch.device) -> torch.Tensor:
-    """Grow-only int32 counters per device, zero-filled once when allocated.
-
-    Each completed decode call leaves the counters it used at zero, so the
-    buffer stays valid for every later shape.  Calls sharing it are ordered on
-    torch's current stream.
-    """
-    idx = _dev_index(device)
-    c = _counters.get(idx)
-    if c is None or c.numel() < count:
-        c = torch.zeros(max(count, 4096), dtype=torch.int32, device=device)
-        _counters[idx] = c
-    return c
 
 
 def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
@@ -241,7 +224,7 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
                  max_seq_len: int, layout: str = "kernel", output: torch.Tensor | None = None,
                  new_keys: torch.Tensor | None = None, new_values: torch.Tensor | None = None,
                  partition_size: int = 0, workspace: torch.Tensor | None = None,
-                 counters: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+                 stream=None) -> torch.Tensor:
     """Paged GQA decode attention, one query token per sequence.
 
     query [num_seqs, H, D] fp16; returns/fills output [num_seqs, H, D].  With
@@ -268,23 +251,17 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
     if query.shape[2] != p.head_size:
         raise ValueError(f"query head_size {query.shape[2]} != cache head_size {p.head_size}")
     nbytes, _ = decode_workspace_size(p)
-    ws_ptr, ws_len, cnt_ptr = None, 0, None
+    ws_ptr, ws_len = None, 0
     if nbytes:
         if workspace is None:
             workspace = decode_workspace(nbytes, query.device)
         if workspace.numel() * workspace.element_size() < nbytes:
             raise ValueError(f"workspace smaller than {nbytes} bytes")
-        ncnt = num_seqs * p.num_kv_heads
-        if counters is None:
-            counters = decode_counters(ncnt, query.device)
-        if counters.dtype != torch.int32 or counters.numel() < ncnt:
-            raise ValueError(f"counters must be int32 with >= {ncnt} zeroed entries")
         ws_ptr, ws_len = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-        cnt_ptr = counters.data_ptr()
     _lib.call("vaa_paged_attention_decode", ctypes.byref(p), query.data_ptr(),
               key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
               seq_lens.data_ptr(), output.data_ptr(), _ptr(new_keys), _ptr(new_values),
-              ws_ptr, ws_len, cnt_ptr, _lib.stream_handle(stream))
+              ws_ptr, ws_len, _lib.stream_handle(stream))
     return output
 
 
