@@ -43,7 +43,32 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="calibration mode: time a plain device-to-device copy of this "
+                         "many bytes instead of the decode step (for HBM counter scaling)")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes: int, steps: int, warmup: int) -> dict:
+    """A plain copy kernel of known size: its FETCH_SIZE/WRITE_SIZE per launch
+    calibrate the PMC-derived HBM traffic of the decode kernel."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"mode": "copy-calibration", "bytes_read_per_launch": nbytes,
+            "bytes_written_per_launch": nbytes, "ms_per_copy": round(ms, 5),
+            "copy_gb_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
 def traffic_from_profile() -> float | None:
@@ -111,6 +136,10 @@ def main() -> int:
                                    "(multi-GPU sharding is design-only, see DESIGN.md)"}))
         return 2
     import torch
+
+    if args.copy_bytes:
+        print(json.dumps(copy_calibration(args.copy_bytes, args.steps, args.warmup)))
+        return 0
 
     from vllm_apple_amd import _lib, kernels, workloads
 
