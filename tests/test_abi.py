@@ -1,0 +1,98 @@
+"""The C-ABI library loads on the CPU and exports every symbol the header declares.
+
+No compute calls: this runs without a GPU.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "vllm_apple_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vaa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from vllm_apple_amd import _lib
+
+    if not _lib.library_path().exists():
+        import vllm_apple_amd
+
+        vllm_apple_amd.build_library(verbose=False)
+    return _lib.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_functions()
+    for must in ("vaa_write_kv_batch", "vaa_write_kv_single", "vaa_kv_write_slots",
+                 "vaa_kv_write_decode", "vaa_paged_attention_decode",
+                 "vaa_paged_attention_decode_workspace_size", "vaa_paged_attention_prefill",
+                 "vaa_rmsnorm", "vaa_rope_neox", "vaa_silu_mul", "vaa_build_token_index",
+                 "vaa_build_slot_mapping", "vaa_last_error", "vaa_abi_version"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+
+
+def test_python_binding_covers_the_header(lib):
+    from vllm_apple_amd import _lib
+
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_params_struct_layout_matches_header():
+    """ctypes mirror of vaa_attn_params: 10 int32/float fields then 13 int64."""
+    from vllm_apple_amd import _lib
+
+    assert ctypes.sizeof(_lib.VaaAttnParams) == 10 * 4 + 13 * 8
+    assert _lib.VaaAttnParams.num_blocks.offset == 40
+
+
+def test_version_and_error_string_without_gpu(lib):
+    assert lib.vaa_abi_version() == 1
+    from vllm_apple_amd import _lib
+
+    assert isinstance(_lib.last_error(), str)
+
+
+def test_argument_errors_are_reported_without_touching_the_gpu(lib):
+    """Bad arguments return VAA_ERR_INVALID_ARG / UNSUPPORTED before any launch."""
+    from vllm_apple_amd import _lib
+
+    p = _lib.VaaAttnParams()
+    p.head_size = 80
+    st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
+                                        None, None, None, 0, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED
+    assert "head_size=80" in _lib.last_error()
+    with pytest.raises(NotImplementedError):
+        _lib.check(st, "decode")
+    st = lib.vaa_rmsnorm(None, None, None, None, 4, 0, 0, 0, 0, 1e-5, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG
+    with pytest.raises(ValueError):
+        _lib.check(st, "rmsnorm")
+    p.head_size = 128
+    p.block_size = 8
+    st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
+                                        None, None, None, 0, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED and "block_size=8" in _lib.last_error()
+
+
+def test_zero_sized_calls_are_noops(lib):
+    from vllm_apple_amd import _lib
+
+    p = _lib.VaaAttnParams()
+    p.num_kv_heads, p.head_size, p.block_size, p.num_blocks = 2, 64, 16, 4
+    assert lib.vaa_kv_write_slots(ctypes.byref(p), None, None, None, 0, None, None, 0, None) == 0
+    assert lib.vaa_silu_mul(None, None, None, 0, None) == 0
+    assert lib.vaa_build_token_index(None, None, 0, 0, None, None, None) == 0

@@ -1,0 +1,273 @@
+"""The drop-in surfaces on the GPU: HipAttentionImpl.forward (vLLM mode) and the
+engine ops (PagedAttentionOp, KVWriteOp, EngineRMSNorm, EngineRoPE,
+EngineElementwiseOps) against the oracle."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import assert_close, host
+
+import oracle.attention as oat
+import oracle.kv as okv
+import oracle.layer_ops as olo
+
+pytestmark = pytest.mark.gpu
+
+
+def _mixed_batch(H=32, KV=8, D=128, bs=16, dec_lens=(37, 300, 1, 2049), pre=((500, 64), (90, 90)),
+                 seed=0, dtype=torch.float16):
+    """vLLM-mode batch: decodes first, then prefill chunks (total len, chunk len)."""
+    g = torch.Generator().manual_seed(seed)
+    lens = list(dec_lens) + [p[0] for p in pre]
+    qlens = [1] * len(dec_lens) + [p[1] for p in pre]
+    nblk = [(L + bs - 1) // bs for L in lens]
+    nb = sum(nblk) + 8
+    kv_cache = torch.randn(2, nb, bs, KV, D, generator=g).to(dtype)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    maxb = max(nblk)
+    bt = torch.full((len(lens), maxb), -1, dtype=torch.int32)
+    off = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[off:off + n]
+        off += n
+    qsl = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    T = int(qsl[-1])
+    tok, pos = okv.token_index(qsl, np.array(lens, np.int32), T)
+    slots = okv.slot_mapping(bt.numpy(), bs, tok, pos)
+    qkv = torch.randn(T, (H + 2 * KV) * D, generator=g).to(dtype)
+    return dict(kv_cache=kv_cache, bt=bt, lens=torch.tensor(lens, dtype=torch.int32),
+                qsl=torch.from_numpy(qsl), slots=torch.from_numpy(slots), qkv=qkv, tok=tok,
+                pos=pos, num_decode=len(dec_lens), T=T, H=H, KV=KV, D=D)
+
+
+def _metadata(b, dev):
+    from vllm_apple_amd.backend import HipAttentionMetadata
+
+    return HipAttentionMetadata(
+        num_actual_tokens=b["T"], max_query_len=int((b["qsl"][1:] - b["qsl"][:-1]).max()),
+        query_start_loc=b["qsl"].to(dev), max_seq_len=int(b["lens"].max()),
+        seq_lens=b["lens"].to(dev), block_table=b["bt"].to(dev),
+        slot_mapping=b["slots"].to(dev), num_decode_tokens=b["num_decode"])
+
+
+def _oracle(b, scale):
+    """KV write through slot_mapping, then decode rows + prefill rows (vLLM layout)."""
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    qkv = b["qkv"].to(torch.float16).numpy()
+    q = qkv[:, :H * D].reshape(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].reshape(T, KV, D)
+    v = qkv[:, (H + KV) * D:].reshape(T, KV, D)
+    kc = b["kv_cache"][0].to(torch.float16).numpy().copy()
+    vc = b["kv_cache"][1].to(torch.float16).numpy().copy()
+    okv.kv_write_slots(kc, vc, k, v, b["slots"].numpy(), "vllm")
+    nd = b["num_decode"]
+    out = np.zeros((T, H, D))
+    out[:nd] = oat.decode(q[:nd], kc, vc, b["bt"].numpy()[:nd], b["lens"].numpy()[:nd], scale,
+                          "vllm")
+    pre, w = oat.prefill(q, kc, vc, b["bt"].numpy(), b["tok"], b["pos"], scale, "vllm",
+                         rows=np.arange(nd, T))
+    out[nd:] = pre[nd:]
+    return out, kc, vc
+
+
+def test_forward_mixed_batch_vllm_cache(gpu):
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    b = _mixed_batch(seed=1)
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    scale = 1 / math.sqrt(D)
+    impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv = b["qkv"].to(dev)
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    kv_cache = b["kv_cache"].to(dev)
+    out = torch.full((T, H, D), 9.0, dtype=torch.float16, device=dev)
+    res = impl.forward(None, q, k, v, kv_cache, _metadata(b, dev), output=out)
+    torch.cuda.synchronize()
+    assert res is out
+    ref, kc, vc = _oracle(b, scale)
+    assert np.array_equal(host(kv_cache[0]).view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(host(kv_cache[1]).view(np.uint16), vc.view(np.uint16))
+    assert_close(host(out), ref, what="forward mixed")
+
+
+def test_forward_bf16_activations(gpu):
+    """bf16 model: activations run in fp16, output copied back to bf16; the
+    bf16 kv_cache is replaced by an fp16 cache of the same shape."""
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    b = _mixed_batch(seed=2, dtype=torch.bfloat16, dec_lens=(40, 7), pre=((64, 20),))
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    scale = 1 / math.sqrt(D)
+    impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv = b["qkv"].to(dev)
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    kv_cache = b["kv_cache"].to(dev)
+    out = torch.zeros((T, H, D), dtype=torch.bfloat16, device=dev)
+    # The fp16 cache starts as a copy of the bf16 cache's contents for this test.
+    impl._shadow = kv_cache.to(torch.float16)
+    impl.forward(None, q, k, v, kv_cache, _metadata(b, dev), output=out)
+    torch.cuda.synchronize()
+    ref, _, _ = _oracle(b, scale)
+    assert out.dtype == torch.bfloat16
+    # bf16 output rounding (8-bit mantissa) on top of the fp16 path.
+    assert_close(host(out.float()), ref, atol=2e-3, rtol=1e-2 + 2 ** -8, what="bf16 forward")
+
+
+def test_forward_encoder_only_bidirectional(gpu):
+    from vllm_apple_amd.backend import AttentionType, HipAttentionImpl, HipAttentionMetadata
+
+    H, KV, D = 8, 2, 64
+    g = torch.Generator().manual_seed(3)
+    lens = [5, 40, 17]
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g).half()
+    k = torch.randn(T, KV, D, generator=g).half()
+    v = torch.randn(T, KV, D, generator=g).half()
+    qsl = torch.tensor([0, 5, 45, 62], dtype=torch.int32)
+    impl = HipAttentionImpl(H, D, 0.125, KV, None, None, "auto",
+                            attn_type=AttentionType.ENCODER_ONLY)
+    dev = torch.device("cuda")
+    md = HipAttentionMetadata(T, 40, qsl.to(dev), 40, torch.tensor(lens).to(dev), None, None)
+    out = torch.zeros(T, H, D, dtype=torch.float16, device=dev)
+    impl.forward(None, q.to(dev), k.to(dev), v.to(dev), None, md, output=out)
+    torch.cuda.synchronize()
+    ref = torch.zeros(T, H, D)
+    for s in range(3):
+        a, e = int(qsl[s]), int(qsl[s + 1])
+        qt = q[a:e].float().transpose(0, 1)
+        kt = k[a:e].float().transpose(0, 1).repeat_interleave(4, 0)
+        vt = v[a:e].float().transpose(0, 1).repeat_interleave(4, 0)
+        ref[a:e] = F.scaled_dot_product_attention(qt, kt, vt, scale=0.125).transpose(0, 1)
+    assert_close(host(out), ref.numpy(), what="encoder-only")
+
+
+def test_engine_ops_planar_qkv_decode_step(gpu):
+    """Engine mode (runner.py:829-1176 order): RMSNorm -> (QKV given) -> RoPE on
+    views of the planar [Q_all][K_all][V_all] buffer -> fused decode."""
+    from vllm_apple_amd.engine import (EngineRMSNorm, EngineRoPE, EngineStepContext,
+                                       PagedAttentionOp)
+
+    H, KV, D, bs, S = 32, 8, 128, 16, 6
+    g = torch.Generator().manual_seed(4)
+    lens = [33, 1000, 16, 4097, 1, 250]
+    nblk = [(L + bs - 1) // bs for L in lens]
+    nb = sum(nblk) + 4
+    kc = torch.randn(nb, KV, bs, D, generator=g).half()
+    vc = torch.randn(nb, KV, bs, D, generator=g).half()
+    maxb = 300
+    bt = torch.full((S, maxb), -1, dtype=torch.int32)
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    off = 0
+    for s, n in enumerate(nblk):
+        bt[s, :n] = perm[off:off + n]
+        off += n
+    qkv = torch.randn(S * (H + 2 * KV) * D, generator=g).half()  # planar
+    positions = torch.tensor([L - 1 for L in lens], dtype=torch.int32)
+    dev = torch.device("cuda")
+    qkv_d, kc_d, vc_d = qkv.to(dev), kc.to(dev), vc.to(dev)
+    out_d = torch.zeros(S * H * D, dtype=torch.float16, device=dev)
+    q_off, k_off, v_off = 0, S * H * D * 2, S * (H + KV) * D * 2
+    rope = EngineRoPE(None, D, H, KV, max_position=8192, base=1e6)
+    attn = PagedAttentionOp(None, KV, H, D, bs)
+    with EngineStepContext() as ctx:
+        rope.encode(ctx, (qkv_d, q_off), (qkv_d, k_off), positions.to(dev), S,
+                    max_position_in_batch=int(positions.max()))
+        attn.encode_decode_fused(ctx, qkv_d, qkv_d, qkv_d, kc_d, vc_d, bt.to(dev),
+                                 torch.tensor(lens, dtype=torch.int32).to(dev), out_d, S,
+                                 max(lens), maxb, query_offset=q_off, new_keys_offset=k_off,
+                                 new_values_offset=v_off)
+        ctx.end_encoding()
+        ctx.wait_until_completed()
+    # Oracle: rope (fp64 from the fp32 table), round to fp16 like the kernel's
+    # in-place store, write K/V at seq_len-1, attend.
+    cos, sin = olo.cos_sin(D, 8192, 1e6)
+    qn = qkv[:S * H * D].view(S, H, D).numpy()
+    kn = qkv[S * H * D:S * (H + KV) * D].view(S, KV, D).numpy()
+    vn = qkv[S * (H + KV) * D:].view(S, KV, D).numpy()
+    qr = olo.rope_neox(qn, positions.numpy(), cos, sin).astype(np.float16)
+    kr = olo.rope_neox(kn, positions.numpy(), cos, sin).astype(np.float16)
+    got_q = host(qkv_d[:S * H * D]).reshape(S, H, D)
+    assert_close(got_q, qr.astype(np.float64), what="rope q (planar view)")
+    kcr, vcr = kc.numpy().copy(), vc.numpy().copy()
+    okv.kv_write_decode(kcr, vcr, host(qkv_d[q_off // 2 + S * H * D:]).reshape(-1)[:S * KV * D]
+                        .reshape(S, KV, D), vn, bt.numpy(), np.array(lens, np.int32))
+    ref = oat.decode(got_q, kcr, vcr, bt.numpy(), np.array(lens, np.int32), 1 / math.sqrt(D))
+    assert_close(host(out_d).reshape(S, H, D), ref, what="engine fused decode")
+    assert np.array_equal(host(kc_d).view(np.uint16), kcr.view(np.uint16))
+    assert_close(host(qkv_d[S * H * D:S * (H + KV) * D]).reshape(S, KV, D),
+                 kr.astype(np.float64), what="rope k (planar view)")
+
+
+def test_engine_prefill_flow_and_layer_ops(gpu):
+    """KVWriteOp.encode_prefill -> PagedAttentionOp.encode_prefill, then
+    EngineRMSNorm (with residual) and encode_silu_mul."""
+    from vllm_apple_amd.engine import (EngineElementwiseOps, EngineRMSNorm, KVWriteOp,
+                                       PagedAttentionOp)
+
+    H, KV, D, bs = 16, 4, 64, 16
+    g = torch.Generator().manual_seed(5)
+    ctx_lens, new = [100, 40], [30, 40]
+    nblk = [(L + bs - 1) // bs for L in ctx_lens]
+    nb = sum(nblk) + 2
+    kc = torch.randn(nb, KV, bs, D, generator=g).half()
+    vc = torch.randn(nb, KV, bs, D, generator=g).half()
+    bt = torch.full((2, max(nblk)), -1, dtype=torch.int32)
+    bt[0, :nblk[0]] = torch.arange(nblk[0], dtype=torch.int32)
+    bt[1, :nblk[1]] = torch.arange(nblk[0], nblk[0] + nblk[1], dtype=torch.int32)
+    qsl = np.array([0, 30, 70], np.int32)
+    tok, pos = okv.token_index(qsl, np.array(ctx_lens, np.int32), 70)
+    slots = okv.slot_mapping(bt.numpy(), bs, tok, pos)
+    q = torch.randn(70, H, D, generator=g).half()
+    nk = torch.randn(70, KV, D, generator=g).half()
+    nv = torch.randn(70, KV, D, generator=g).half()
+    dev = torch.device("cuda")
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    out = torch.zeros(70, H, D, dtype=torch.float16, device=dev)
+    KVWriteOp(None, KV, D, bs).encode_prefill(None, nk.to(dev), nv.to(dev), kc_d, vc_d,
+                                              torch.from_numpy(slots).to(torch.int32).to(dev), 70)
+    PagedAttentionOp(None, KV, H, D, bs).encode_prefill(
+        None, q.to(dev), kc_d, vc_d, bt.to(dev), torch.from_numpy(tok).to(dev),
+        torch.from_numpy(pos).to(dev), out, 70, 2, 100, bt.shape[1])
+    x = torch.randn(70, 512, generator=g).half()
+    r = torch.randn(70, 512, generator=g).half()
+    w = (torch.randn(512, generator=g) * 0.1 + 1).half()
+    y = torch.empty(70, 512, dtype=torch.float16, device=dev)
+    norm = EngineRMSNorm(None, 512, eps=1e-5, weight_buffer=w.to(dev))
+    norm.encode(None, x.to(dev), y, 70, residual_buffer=r.to(dev))
+    gate = torch.randn(70 * 256, generator=g).half()
+    up = torch.randn(70 * 256, generator=g).half()
+    act = torch.empty(70 * 256, dtype=torch.float16, device=dev)
+    EngineElementwiseOps(None).encode_silu_mul(None, gate.to(dev), up.to(dev), act, 70 * 256)
+    torch.cuda.synchronize()
+    kr, vr = kc.numpy().copy(), vc.numpy().copy()
+    okv.kv_write_slots(kr, vr, nk.numpy(), nv.numpy(), slots)
+    assert np.array_equal(host(kc_d).view(np.uint16), kr.view(np.uint16))
+    ref, _ = oat.prefill(q.numpy(), kr, vr, bt.numpy(), tok, pos, 1 / 8)
+    assert_close(host(out), ref, what="engine prefill")
+    assert_close(host(y), olo.rms_norm(x.numpy(), w.numpy(), 1e-5, r.numpy()), what="rmsnorm")
+    assert_close(host(act), olo.silu_mul(gate.numpy(), up.numpy()), what="silu_mul")
+
+
+def test_kv_cache_object_write_and_validate(gpu):
+    from vllm_apple_amd.kv_cache import HipKVCache, KVCacheDescriptor
+
+    c = HipKVCache(KVCacheDescriptor(16, 16, 4, 128, 2))
+    key = np.full((4, 128), 1.5, np.float16)
+    val = np.full((4, 128), 2.5, np.float16)
+    c.write_kv(1, 3, 5, torch.from_numpy(key), torch.from_numpy(val))  # known answer
+    torch.cuda.synchronize()
+    k, v = c.get_buffers(1)
+    assert torch.all(k[3, :, 5] == 1.5) and torch.all(v[3, :, 5] == 2.5)
+    assert int(torch.count_nonzero(k)) == 4 * 128
+    assert int(torch.count_nonzero(c.get_key_buffer(0))) == 0
+    with pytest.raises(ValueError):
+        c.write_kv(0, 0, 16, torch.from_numpy(key), torch.from_numpy(val))

@@ -1,0 +1,197 @@
+"""Host-side logic on the CPU: validation rules, strides, parameter packing,
+metadata construction and the backend's static surface and error conventions.
+
+Cases follow the reference's own unit tests (tests/unit/test_engine.py:320-423)
+and the error behaviour of metal_attn.py / engine/kv_cache.py.
+"""
+import struct
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from vllm_apple_amd import backend, indexing
+from vllm_apple_amd.engine.attention import (FusedAttentionParams, PagedAttentionOp,
+                                             PagedAttentionParams)
+from vllm_apple_amd.engine.kv_write import KVWriteParams
+from vllm_apple_amd.kv_cache import HipKVCache, KVCacheDescriptor
+
+
+def _cache(num_blocks=100, block_size=16):
+    return HipKVCache(KVCacheDescriptor(num_blocks, block_size, 2, 64, 1), device="cpu")
+
+
+# -- KV cache validation (engine/kv_cache.py:300-420, test_engine.py:343-423) --------
+def test_valid_slot_mapping():
+    _cache().validate_slot_mapping(np.array([0, 1, 15, 100, 1599], dtype=np.int32))
+
+
+def test_invalid_slot_oob():
+    with pytest.raises(ValueError, match="Slot mapping contains index 2000"):
+        _cache().validate_slot_mapping(np.array([0, 1, 2000], dtype=np.int32))
+
+
+def test_negative_one_slot_allowed_and_minus_two_rejected():
+    c = _cache()
+    c.validate_slot_mapping(np.array([0, -1, 10, -1, 20], dtype=np.int32))
+    with pytest.raises(ValueError, match="invalid index -2"):
+        c.validate_slot_mapping(np.array([0, -2, 10], dtype=np.int32))
+
+
+def test_slot_mapping_torch_and_empty():
+    c = _cache()
+    c.validate_slot_mapping(torch.tensor([0, 10, 100], dtype=torch.int32))
+    c.validate_slot_mapping(np.array([], dtype=np.int32))
+
+
+def test_block_table_validation():
+    c = _cache(num_blocks=8)
+    c.validate_block_table(np.array([[0, 7, -1]], dtype=np.int32))
+    with pytest.raises(ValueError, match="Block table contains index 8 >= num_blocks 8"):
+        c.validate_block_table(np.array([[0, 8]], dtype=np.int32))
+    with pytest.raises(ValueError, match="invalid index -3"):
+        c.validate_block_table(torch.tensor([[0, -3]], dtype=torch.int32))
+
+
+def test_descriptor_rules():
+    with pytest.raises(ValueError, match="head_size must be 32/64/96/128"):
+        KVCacheDescriptor(4, 16, 2, 80, 1)
+    with pytest.raises(ValueError, match="num_blocks must be >= 1"):
+        KVCacheDescriptor(0, 16, 2, 64, 1)
+    d = KVCacheDescriptor(10, 16, 8, 128, 2)
+    assert d.block_size_bytes == 8 * 16 * 128 * 2 * 2
+    assert d.total_cache_bytes == d.block_size_bytes * 10 * 2
+
+
+def test_strides_match_reference():
+    """test_engine.py:320-341."""
+    c = HipKVCache(KVCacheDescriptor(4, 16, 8, 128, 1), device="cpu")
+    assert c.strides["block"] == 16384 and c.strides["head"] == 2048 and c.strides["token"] == 128
+    k, v = c.get_buffers(0)
+    assert k.shape == (4, 8, 16, 128)
+    assert k.stride()[:3] == (16384, 2048, 128)
+    assert c.get_slot_offset(37) == (2, 5)
+    assert c.get_element_offset(2, 3, 5) == 2 * 16384 + 3 * 2048 + 5 * 128
+    op = PagedAttentionOp(None, 8, 32, 128, 16)
+    assert (op.new_kv_stride_token, op.new_kv_stride_head) == (1024, 128)
+
+
+# -- parameter structs keep the reference packing ------------------------------------
+def test_param_struct_packing():
+    op = PagedAttentionOp(None, num_kv_heads=8, num_query_heads=32, head_size=128,
+                          block_size=16)
+    fp = op.fused_params(num_seqs=4, max_seq_len=100, max_blocks_per_seq=7)
+    raw = fp.to_bytes()
+    assert len(raw) == 4 + 20 * 4
+    vals = struct.unpack("f" + "I" * 20, raw)
+    assert vals[1:9] == (4, 100, 7, 128, 16, 8, 32, 4)
+    assert abs(vals[0] - 1 / 128 ** 0.5) < 1e-7
+    pp = PagedAttentionParams(*([1.0] + [2] * 18))
+    assert len(pp.to_bytes()) == 4 + 18 * 4
+    kp = KVWriteParams(1, 2, 3, 4, 5, 6, 7, 8, 9)
+    assert struct.unpack("I" * 9, kp.to_bytes()) == (1, 2, 3, 4, 5, 6, 7, 8, 9)
+    assert isinstance(fp, FusedAttentionParams)
+
+
+# -- index rules (runner.py:526-683, apple_model_runner.py:1188-1278) ---------------
+def test_token_to_seq_rules():
+    tok = indexing.derive_token_to_seq(torch.tensor([0, 3, 3, 5]), 3, 5)
+    assert tok.tolist() == [0, 0, 0, 2, 2]
+    with pytest.raises(ValueError, match="expected 4"):
+        indexing.derive_token_to_seq(torch.tensor([0, 3, 5]), 3, 5)
+    with pytest.raises(ValueError, match="must be 0"):
+        indexing.derive_token_to_seq(torch.tensor([1, 3, 5]), 2, 5)
+    with pytest.raises(ValueError, match="must equal num_tokens"):
+        indexing.derive_token_to_seq(torch.tensor([0, 3, 4]), 2, 5)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        indexing.derive_token_to_seq(torch.tensor([0, 4, 3, 5]), 3, 5)
+    with pytest.raises(ValueError, match="requires query_start_locs"):
+        indexing.derive_token_to_seq(None, 1, 1)
+
+
+def test_positions_and_capacity():
+    pos = indexing.positions_from_lengths(torch.tensor([0, 1, 4]), torch.tensor([513, 10]))
+    assert pos.tolist() == [512, 7, 8, 9]
+    bt = torch.zeros((2, 4), dtype=torch.int32)
+    assert indexing.check_block_capacity(torch.tensor([64, 10]), bt, 16) == 64
+    with pytest.raises(ValueError, match="exceeds block_table capacity"):
+        indexing.check_block_capacity(torch.tensor([65]), bt[:1], 16)
+
+
+def test_slot_mapping_and_block_table_from_lists():
+    slots = indexing.slot_mapping_from_blocks([[7, 2], [5]], [[0, 17, 40], [15, 16]], 16)
+    assert slots.tolist() == [112, 33, 40, 95, 16]
+    bt = indexing.block_table_from_lists([[7, 2], [], [5]])
+    assert bt.tolist() == [[7, 2], [-1, -1], [5, -1]]
+
+
+# -- backend static surface (metal_attn.py:124-199) ----------------------------------
+def test_backend_surface():
+    B = backend.HipAttentionBackend
+    assert B.accept_output_buffer is True
+    assert B.get_supported_dtypes() == [torch.float16, torch.bfloat16]
+    assert B.get_supported_head_sizes() == [32, 64, 96, 128]
+    assert B.get_kv_cache_shape(10, 16, 8, 128) == (2, 10, 16, 8, 128)
+    assert B.use_cascade_attention() is False
+    assert B.get_kv_cache_device() == "cuda"
+    assert B.get_impl_cls() is backend.HipAttentionImpl
+    assert B.get_builder_cls() is backend.HipAttentionMetadataBuilder
+    assert B.supports_attn_type(backend.AttentionType.DECODER)
+    assert not B.supports_attn_type(backend.AttentionType.ENCODER_DECODER)
+
+
+def _impl(**kw):
+    args = dict(num_heads=32, head_size=128, scale=0.1, num_kv_heads=8, alibi_slopes=None,
+                sliding_window=None, kv_cache_dtype="auto")
+    args.update(kw)
+    return backend.HipAttentionImpl(**args)
+
+
+def test_impl_error_conventions():
+    with pytest.raises(NotImplementedError, match="FP8"):
+        _impl(kv_cache_dtype="fp8")
+    with pytest.raises(ValueError):
+        _impl(head_size=80)
+    impl = _impl(sliding_window=4096)
+    assert impl.sliding_window == (4095, 0)
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    out = torch.ones_like(q)
+    with pytest.raises(AssertionError):
+        impl.forward(None, q, q[:, :8], q[:, :8], None, None, output=None)
+    with pytest.raises(NotImplementedError):
+        impl.forward(None, q, q[:, :8], q[:, :8], None, None, output=out, output_scale=q)
+    # attn_metadata None (warm-up): output returned untouched
+    assert impl.forward(None, q, q[:, :8], q[:, :8], None, None, output=out) is out
+    assert torch.all(out == 1)
+
+
+def test_split_decodes_and_prefills():
+    f = backend.split_decodes_and_prefills
+    assert f([0, 1, 2, 3]) == (3, 0, 3, 0)
+    assert f([0, 1, 2, 10, 12]) == (2, 2, 2, 10)
+    assert f([0, 5, 9]) == (0, 2, 0, 9)
+    assert f([0]) == (0, 0, 0, 0)
+
+
+def test_metadata_builder():
+    cm = SimpleNamespace(num_actual_tokens=12, max_query_len=8,
+                         query_start_loc=torch.tensor([0, 1, 2, 10, 12], dtype=torch.int32),
+                         query_start_loc_cpu=torch.tensor([0, 1, 2, 10, 12]),
+                         max_seq_len=900, seq_lens=torch.tensor([5, 900, 8, 2]),
+                         seq_lens_cpu=torch.tensor([5, 900, 8, 2]),
+                         block_table_tensor=torch.zeros(4, 57, dtype=torch.int32),
+                         slot_mapping=torch.zeros(12, dtype=torch.int64), causal=True)
+    md = backend.HipAttentionMetadataBuilder().build(0, cm)
+    assert md.num_decode_tokens == 2 and md.num_actual_tokens == 12
+    assert md.query_start_loc_cpu == [0, 1, 2, 10, 12]
+    assert md.seq_lens_cpu == [5, 900, 8, 2]
+
+
+def test_ops_reject_cpu_tensors():
+    """No CPU fallback: the HIP path refuses host tensors loudly."""
+    from vllm_apple_amd import kernels
+
+    x = torch.zeros(4, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        kernels.rms_norm(x, torch.ones(128, dtype=torch.float16), 1e-6)

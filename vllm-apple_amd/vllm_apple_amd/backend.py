@@ -1,0 +1,334 @@
+"""vLLM attention backend on the HIP kernels: drop-in for METAL_ATTN.
+
+Mirrors vllm_apple/v1/attention/backends/metal_attn.py:
+  HipAttentionBackend           MetalAttentionBackend (:124-199)
+  HipAttentionMetadata          MetalAttentionMetadata (:202-250)
+  HipAttentionMetadataBuilder   MetalAttentionMetadataBuilder (:253-321)
+  HipAttentionImpl              MetalAttentionImpl (:324-764), forward (:568-764)
+
+Differences from the Metal backend, all on the device side:
+  * vLLM's own kv_cache tensor [2, num_blocks, block_size, num_kv_heads, D] is
+    read and written directly in HBM (the kernels take its strides), so there
+    is no shadow cache and no host copy; the KV write is one launch.
+  * Chunked-prefill tokens attend to the cached prefix plus the causal chunk
+    (paged_attention_v2.metal:375-478 semantics) instead of the chunk alone.
+  * Every call only enqueues on the current HIP stream; nothing synchronises.
+vLLM is optional at import time: without it the classes use local stand-ins
+for AttentionType and the abstract bases.
+"""
+from __future__ import annotations
+
+import logging
+from dataclasses import dataclass
+from typing import Any, ClassVar, Optional
+
+import torch
+
+from . import kernels
+
+logger = logging.getLogger(__name__)
+
+try:  # pragma: no cover - vLLM is not installed in the build container
+    from vllm.attention.backends.abstract import (AttentionBackend, AttentionImpl,
+                                                  AttentionType)
+except Exception:  # noqa: BLE001
+    AttentionBackend = object
+    AttentionImpl = object
+
+    class AttentionType:  # vllm/attention/backends/abstract.py values
+        DECODER = "decoder"
+        ENCODER = "encoder"
+        ENCODER_ONLY = "encoder_only"
+        ENCODER_DECODER = "encoder_decoder"
+
+
+SUPPORTED_HEAD_SIZES = [32, 64, 96, 128]
+BACKEND_NAME = "VAA_HIP_ATTN"
+
+
+def is_quantized_kv_cache(kv_cache_dtype: str) -> bool:
+    return kv_cache_dtype not in ("auto", "float16", "half", "fp16", "bfloat16", "bf16")
+
+
+class HipAttentionBackend(AttentionBackend):
+    accept_output_buffer: bool = True
+    supported_dtypes: ClassVar[list] = [torch.float16, torch.bfloat16]
+
+    @classmethod
+    def get_supported_dtypes(cls) -> list:
+        return [torch.float16, torch.bfloat16]
+
+    @classmethod
+    def get_supported_head_sizes(cls) -> list:
+        return list(SUPPORTED_HEAD_SIZES)
+
+    @staticmethod
+    def get_name() -> str:
+        return BACKEND_NAME
+
+    @classmethod
+    def supports_attn_type(cls, attn_type: str) -> bool:
+        return attn_type in (AttentionType.DECODER, AttentionType.ENCODER,
+                             AttentionType.ENCODER_ONLY)
+
+    @staticmethod
+    def get_impl_cls():
+        return HipAttentionImpl
+
+    @staticmethod
+    def get_builder_cls():
+        return HipAttentionMetadataBuilder
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int,
+                           cache_dtype_str: str = "auto") -> tuple:
+        """[2, num_blocks, block_size, num_kv_heads, head_size] (metal_attn.py:171-185)."""
+        return 2, num_blocks, block_size, num_kv_heads, head_size
+
+    @staticmethod
+    def use_cascade_attention(*args, **kwargs) -> bool:
+        return False
+
+    @staticmethod
+    def get_kv_cache_device() -> str:
+        """The cache lives in HBM (the Metal backend returns "cpu": unified memory)."""
+        return "cuda"
+
+
+@dataclass
+class HipAttentionMetadata:
+    num_actual_tokens: int
+    max_query_len: int
+    query_start_loc: torch.Tensor
+    max_seq_len: int
+    seq_lens: torch.Tensor
+    block_table: torch.Tensor
+    slot_mapping: torch.Tensor
+    scheduler_metadata: Optional[torch.Tensor] = None
+    causal: bool = True
+    num_decode_tokens: int = 0
+    _query_start_loc_cpu: Optional[list] = None
+    _seq_lens_cpu: Optional[list] = None
+
+    @property
+    def query_start_loc_cpu(self) -> list:
+        if self._query_start_loc_cpu is None:
+            self._query_start_loc_cpu = self.query_start_loc.tolist()
+        return self._query_start_loc_cpu
+
+    @property
+    def seq_lens_cpu(self) -> list:
+        if self._seq_lens_cpu is None:
+            self._seq_lens_cpu = self.seq_lens.tolist()
+        return self._seq_lens_cpu
+
+
+def split_decodes_and_prefills(query_start_loc_cpu: list, decode_threshold: int = 1):
+    """(num_decodes, num_prefills, num_decode_tokens, num_prefill_tokens) for a
+    batch whose decode requests come first, as vLLM's reorder guarantees.
+
+    Restates the behaviour of vLLM's split_decodes_and_prefills, which the
+    reference calls (metal_attn.py:302-308); vLLM is not vendored, so this
+    boundary is not pinned by a reference test.
+    """
+    qsl = list(query_start_loc_cpu)
+    num_reqs = len(qsl) - 1
+    num_tokens = qsl[-1] if qsl else 0
+    lens = [qsl[i + 1] - qsl[i] for i in range(num_reqs)]
+    first_prefill = next((i for i, n in enumerate(lens) if n > decode_threshold), num_reqs)
+    num_decode_tokens = qsl[first_prefill] if num_reqs else 0
+    return (first_prefill, num_reqs - first_prefill, num_decode_tokens,
+            num_tokens - num_decode_tokens)
+
+
+class HipAttentionMetadataBuilder:
+    """Builds HipAttentionMetadata from vLLM's CommonAttentionMetadata."""
+
+    reorder_batch_threshold: int = 1
+
+    def __init__(self, kv_cache_spec: Any = None, layer_names: Optional[list] = None,
+                 vllm_config: Any = None, device: Optional[torch.device] = None):
+        self.kv_cache_spec = kv_cache_spec
+        self.layer_names = layer_names or []
+        self.vllm_config = vllm_config
+        self.device = device
+        self.block_size = getattr(kv_cache_spec, "block_size", 16)
+
+    def build(self, common_prefix_len: int, common_attn_metadata: Any,
+              fast_build: bool = False) -> HipAttentionMetadata:
+        cm = common_attn_metadata
+        qsl_cpu = getattr(cm, "query_start_loc_cpu", None)
+        if qsl_cpu is None:
+            qsl_cpu = cm.query_start_loc.cpu()
+        qsl_list = qsl_cpu.tolist() if isinstance(qsl_cpu, torch.Tensor) else list(qsl_cpu)
+        num_decode_tokens = 0
+        if cm.causal:
+            _, _, num_decode_tokens, _ = split_decodes_and_prefills(
+                qsl_list, self.reorder_batch_threshold)
+        seq_cpu = getattr(cm, "seq_lens_cpu", None)
+        return HipAttentionMetadata(
+            num_actual_tokens=cm.num_actual_tokens,
+            max_query_len=cm.max_query_len,
+            query_start_loc=cm.query_start_loc,
+            max_seq_len=cm.max_seq_len,
+            seq_lens=cm.seq_lens,
+            block_table=cm.block_table_tensor,
+            slot_mapping=cm.slot_mapping,
+            scheduler_metadata=None,
+            causal=cm.causal,
+            num_decode_tokens=num_decode_tokens,
+            _query_start_loc_cpu=qsl_list,
+            _seq_lens_cpu=seq_cpu.tolist() if isinstance(seq_cpu, torch.Tensor) else seq_cpu,
+        )
+
+
+class HipAttentionImpl(AttentionImpl):
+    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
+                 alibi_slopes: Optional[list], sliding_window: Optional[int],
+                 kv_cache_dtype: str, logits_soft_cap: Optional[float] = None,
+                 attn_type: str = AttentionType.DECODER,
+                 kv_sharing_target_layer_name: Optional[str] = None,
+                 sinks: Optional[torch.Tensor] = None) -> None:
+        self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+        self._is_kv_shared = kv_sharing_target_layer_name is not None
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        if logits_soft_cap is not None:
+            logger.warning("%s does not support logits softcap, outputs may be slightly off",
+                           BACKEND_NAME)
+        self.logits_soft_cap = logits_soft_cap or 0
+        self.num_kv_heads = num_kv_heads
+        if alibi_slopes is not None:
+            logger.warning("%s does not support ALiBi slopes, ignoring", BACKEND_NAME)
+        self.alibi_slopes = None
+        if sliding_window is None:
+            self.sliding_window = (-1, -1)
+        elif attn_type == AttentionType.ENCODER_ONLY:
+            self.sliding_window = (sliding_window - 1, sliding_window - 1)
+        else:
+            self.sliding_window = (sliding_window - 1, 0)
+        self.kv_cache_dtype = kv_cache_dtype
+        self.num_queries_per_kv = num_heads // num_kv_heads
+        if is_quantized_kv_cache(kv_cache_dtype):
+            raise NotImplementedError(f"FP8 KV cache is unsupported in {BACKEND_NAME}")
+        if head_size not in SUPPORTED_HEAD_SIZES:
+            raise ValueError(f"head_size must be 32/64/96/128, got {head_size}")
+        if num_heads % num_kv_heads != 0 or self.num_queries_per_kv > 16:
+            raise NotImplementedError(
+                f"num_heads={num_heads}, num_kv_heads={num_kv_heads}: GQA groups up to 16")
+        self.attn_type = attn_type
+        self.sinks = sinks
+        self._shadow: Optional[torch.Tensor] = None
+
+    # ------------------------------------------------------------------ cache
+    def _caches(self, kv_cache: torch.Tensor) -> tuple:
+        """(key_cache, value_cache) in the vLLM layout [nb, bs, KV, D], fp16.
+
+        An fp16 kv_cache is used in place.  For any other cache dtype (bf16
+        models) a same-shaped fp16 cache is kept per layer, as the Metal
+        backend keeps its own fp16 cache (metal_attn.py:654-660).
+        """
+        if kv_cache.dtype == torch.float16:
+            return kv_cache[0], kv_cache[1]
+        if self._shadow is None or self._shadow.shape != kv_cache.shape:
+            self._shadow = torch.zeros(kv_cache.shape, dtype=torch.float16,
+                                       device=kv_cache.device)
+        return self._shadow[0], self._shadow[1]
+
+    # ---------------------------------------------------------------- forward
+    def forward(self, layer: Any, query: torch.Tensor, key: Optional[torch.Tensor],
+                value: Optional[torch.Tensor], kv_cache: torch.Tensor,
+                attn_metadata: Optional[HipAttentionMetadata],
+                output: Optional[torch.Tensor] = None,
+                output_scale: Optional[torch.Tensor] = None,
+                output_block_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+        assert output is not None, "Output tensor must be provided."
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError(
+                "Fused output quantization is not yet supported for HipAttentionImpl")
+        if attn_metadata is None:  # warm-up / profiling
+            return output
+
+        # bf16 activations run through the fp16 kernels (metal_attn.py:609-620).
+        original_output = output
+        conv = query.dtype == torch.bfloat16
+        if conv:
+            query = query.to(torch.float16)
+            key = key.to(torch.float16) if key is not None else None
+            value = value.to(torch.float16) if value is not None else None
+            output = torch.empty(output.shape, dtype=torch.float16, device=output.device)
+
+        n = attn_metadata.num_actual_tokens
+        if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
+            self._attention_no_cache(query[:n], key[:n], value[:n], output[:n], attn_metadata,
+                                     causal=False)
+        else:
+            key_cache, value_cache = self._caches(kv_cache)
+            if not self._is_kv_shared and key is not None and value is not None and n > 0:
+                kernels.kv_write_slots(key[:n], value[:n], key_cache, value_cache,
+                                       attn_metadata.slot_mapping[:n], layout="vllm")
+            nd = attn_metadata.num_decode_tokens
+            if nd > 0:
+                kernels.paged_decode(query[:nd], key_cache, value_cache,
+                                     attn_metadata.block_table[:nd],
+                                     attn_metadata.seq_lens[:nd], scale=self.scale,
+                                     max_seq_len=attn_metadata.max_seq_len, layout="vllm",
+                                     output=output[:nd])
+            if n > nd:
+                tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,
+                                                     attn_metadata.seq_lens, n)
+                kernels.paged_prefill(query[nd:n], key_cache, value_cache,
+                                      attn_metadata.block_table, tok[nd:n], pos[nd:n],
+                                      scale=self.scale, layout="vllm", output=output[nd:n])
+        if conv:
+            original_output[:n].copy_(output[:n].to(original_output.dtype))
+            return original_output
+        return output
+
+    def _attention_no_cache(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                            output: torch.Tensor, attn_metadata: HipAttentionMetadata,
+                            causal: bool) -> torch.Tensor:
+        """Attention inside each sequence's own tokens (encoder / no KV cache),
+        the semantics of _compute_attention_sdpa (base_attn.py:223-306).
+
+        The tokens are staged into a scratch paged cache, one block-aligned
+        range per sequence, and run through the prefill kernel; positions are
+        the in-sequence index (causal) or the last index (bidirectional).
+        """
+        qsl = attn_metadata.query_start_loc_cpu
+        num_seqs = len(qsl) - 1
+        bs = 16
+        blk_off, nblk = [], []
+        total = 0
+        for s in range(num_seqs):
+            n = qsl[s + 1] - qsl[s]
+            blk_off.append(total)
+            nblk.append((n + bs - 1) // bs)
+            total += nblk[-1]
+        T = query.shape[0]
+        if T == 0 or total == 0:
+            return output
+        maxb = max(max(nblk), 1)
+        slots, tok, pos = [], [], []
+        bt = [[-1] * maxb for _ in range(num_seqs)]
+        for s in range(num_seqs):
+            n = qsl[s + 1] - qsl[s]
+            for i in range(nblk[s]):
+                bt[s][i] = blk_off[s] + i
+            for i in range(n):
+                slots.append(blk_off[s] * bs + i)
+                tok.append(s)
+                pos.append(i if causal else n - 1)
+        dev = query.device
+        kv = key.shape[1]
+        kc = torch.empty((total, bs, kv, self.head_size), dtype=torch.float16, device=dev)
+        vc = torch.empty_like(kc)
+        slot_t = torch.tensor(slots, dtype=torch.int64).to(dev, non_blocking=True)
+        bt_t = torch.tensor(bt, dtype=torch.int32).to(dev, non_blocking=True)
+        tok_t = torch.tensor(tok, dtype=torch.int32).to(dev, non_blocking=True)
+        pos_t = torch.tensor(pos, dtype=torch.int32).to(dev, non_blocking=True)
+        kernels.kv_write_slots(key, value, kc, vc, slot_t[:T], layout="vllm")
+        kernels.paged_prefill(query, kc, vc, bt_t, tok_t[:T], pos_t[:T], scale=self.scale,
+                              layout="vllm", output=output)
+        return output

@@ -1,0 +1,27 @@
+"""Encode-only ops mirroring vllm_apple/engine/ops/{attention,kv_write,rmsnorm,elementwise}.py.
+
+"Encode" here means: enqueue the HIP kernels on a stream and return without
+waiting.  Every encode_* method keeps the reference's argument names and order;
+its first argument, step_ctx, may be None (torch's current stream), a
+torch.cuda.Stream, or any object with a `.stream` attribute.  Buffers are fp16
+or int32 torch tensors on the GPU; byte offsets select a view into them like
+the reference's (MTLBuffer, offset) pairs.
+"""
+from .attention import FusedAttentionParams, PagedAttentionOp, PagedAttentionParams
+from .elementwise import EngineElementwiseOps, EngineRoPE
+from .kv_write import KVWriteOp, KVWriteParams
+from .rmsnorm import EngineRMSNorm, RMSNormConfig
+from .step import EngineStepContext
+
+__all__ = [
+    "EngineElementwiseOps",
+    "EngineRMSNorm",
+    "EngineRoPE",
+    "EngineStepContext",
+    "FusedAttentionParams",
+    "KVWriteOp",
+    "KVWriteParams",
+    "PagedAttentionOp",
+    "PagedAttentionParams",
+    "RMSNormConfig",
+]

@@ -1,0 +1,63 @@
+"""EngineRMSNorm: mirror of vllm_apple/engine/ops/rmsnorm.py on HIP.
+
+encode (rmsnorm.py:226-321): out = x * rsqrt(mean(x^2) + eps) * w, plus the
+residual added after the norm when residual_buffer is given (the reference's
+rmsnorm_residual_kernel, :128-173).  One wave per row, row kept in registers.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Dict, Optional
+
+import torch
+
+from .. import kernels
+from .step import resolve_stream, view
+
+
+@dataclass
+class RMSNormConfig:
+    hidden_size: int
+    eps: float = 1e-6
+    dtype: torch.dtype = torch.float16
+
+
+class EngineRMSNorm:
+    def __init__(self, context: Any, hidden_size: int, eps: float = 1e-6,
+                 weight_buffer: Optional[torch.Tensor] = None):
+        self._context = context
+        self.config = RMSNormConfig(hidden_size=hidden_size, eps=eps)
+        self._weight_buffer = weight_buffer
+
+    def set_weights(self, weight_buffer: torch.Tensor) -> None:
+        self._weight_buffer = weight_buffer
+
+    @staticmethod
+    def _buf(x: Any):
+        """Accept a tensor or an (tensor, byte_offset) pair."""
+        if isinstance(x, tuple):
+            return x
+        return x, 0
+
+    def encode(self, step_ctx: Any, input_buffer: Any, output_buffer: Any, num_tokens: int,
+               residual_buffer: Optional[Any] = None) -> None:
+        if self._weight_buffer is None:
+            raise RuntimeError("Weights not set - call set_weights() first")
+        stream = resolve_stream(step_ctx)
+        H = self.config.hidden_size
+        ib, io = self._buf(input_buffer)
+        ob, oo = self._buf(output_buffer)
+        x = view(ib, io, (num_tokens, H))
+        out = view(ob, oo, (num_tokens, H))
+        res = None
+        if residual_buffer is not None:
+            rb, ro = self._buf(residual_buffer)
+            res = view(rb, ro, (num_tokens, H))
+        w = self._weight_buffer.reshape(-1)[:H]
+        kernels.rms_norm(x, w, self.config.eps, residual=res, out=out, stream=stream)
+
+    def get_output_size(self, num_tokens: int) -> int:
+        return num_tokens * self.config.hidden_size * 2
+
+    def get_params_dict(self) -> Dict[str, Any]:
+        return {"hidden_size": self.config.hidden_size, "eps": self.config.eps}
