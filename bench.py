@@ -43,6 +43,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="headline",
+                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "all"],
+                    help="headline = the contract line; the others print one JSON line per "
+                         "BASELINE config (measurement record, not the driver's metric)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="calibration mode: time a plain device-to-device copy of this "
                          "many bytes instead of the decode step (for HBM counter scaling)")
@@ -129,6 +133,168 @@ def cpu_baseline(batch, budget_s: float) -> dict:
     }
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def _timed(fn, steps: int, warmup: int) -> float:
+    """Average duration (ms) of fn's launches from HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+
+
+def _decode_record(name: str, b, args, partition: int, note: str) -> dict:
+    import torch
+
+    from vllm_apple_amd import kernels
+
+    out = torch.empty_like(b.query)
+    lens = b.extra["seq_lens_host"]
+
+    def step():
+        kernels.paged_decode(b.query, b.k_cache, b.v_cache, b.block_table, b.seq_lens,
+                             scale=b.scale, max_seq_len=b.max_seq_len, output=out,
+                             new_keys=b.new_k, new_values=b.new_v, partition_size=partition,
+                             seq_lens_host=lens)
+
+    ms = _timed(step, args.steps, args.warmup)
+    alg = b.decode_algorithmic_bytes()
+    used = partition or kernels.choose_partition_size(lens, b.num_kv_heads,
+                                                      kernels.device_cus(b.query.device))
+    return {"workload": name, "note": note, "batch": b.num_seqs,
+            "ctx_mean": round(sum(lens) / len(lens), 1), "ctx_max": max(lens),
+            "partition": used, "ms_per_step": round(ms, 5),
+            "algorithmic_bytes": alg, "gb_s": round(alg / (ms * 1e-3) / 1e9, 1),
+            "pct_hbm_peak": round(100 * alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "tokens_per_s": round(b.num_seqs / (ms * 1e-3), 1)}
+
+
+def wl_c1(args) -> dict:
+    import torch
+
+    from vllm_apple_amd import workloads
+
+    b = workloads.c1_decode(device=torch.device("cuda:0"))
+    r = _decode_record("C1", b, args, 0, "Qwen2-0.5B decode, B=4, cache-resident: latency")
+    r["latency_us"] = round(r["ms_per_step"] * 1e3, 2)
+    return r
+
+
+def wl_c2u(args) -> dict:
+    import torch
+
+    from vllm_apple_amd import workloads
+
+    b = workloads.c2_decode(device=torch.device("cuda:0"))
+    return _decode_record("C2u", b, args, 0, "ctx U{1024..8192}, split-K chosen from lengths")
+
+
+def wl_c4(args) -> dict:
+    import torch
+
+    from vllm_apple_amd import workloads
+
+    b = workloads.c4_long_decode(device=torch.device("cuda:0"))
+    r512 = _decode_record("C4", b, args, 512, "512-token partitions + LSE merge (config spec)")
+    rauto = _decode_record("C4", b, args, 0, "partition chosen from lengths")
+    r512["auto_partition"] = {k: rauto[k] for k in ("partition", "ms_per_step", "gb_s",
+                                                   "pct_hbm_peak")}
+    r512["scaled_key_rows"] = b.extra["scaled_rows"]
+    return r512
+
+
+def _prefill_flops(b) -> float:
+    """Causal-exact: 4 * D per (query token, head, attended key)."""
+    ctx = (b.positions.double() + 1).sum().item()
+    return 4.0 * b.head_size * b.num_q_heads * ctx
+
+
+def wl_c3(args) -> dict:
+    import torch
+
+    from vllm_apple_amd import kernels, workloads
+
+    b = workloads.c3_prefill(device=torch.device("cuda:0"))
+    out = torch.empty_like(b.query)
+    t_kv = _timed(lambda: kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache,
+                                                 b.slot_mapping), args.steps, args.warmup)
+    t_at = _timed(lambda: kernels.paged_prefill(b.query, b.k_cache, b.v_cache, b.block_table,
+                                                b.token_to_seq, b.positions, scale=b.scale,
+                                                output=out), args.steps, args.warmup)
+    fl = _prefill_flops(b)
+    T = b.query.shape[0]
+    kv_bytes = 2 * 2 * T * b.num_kv_heads * b.head_size * 2 + T * 8
+    return {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
+            "tokens": T, "kv_write_ms": round(t_kv, 5),
+            "kv_write_gb_s": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
+            "prefill_ms": round(t_at, 5), "flops": fl,
+            "tflop_s": round(fl / (t_at * 1e-3) / 1e12, 1),
+            "mfma_util_pct": round(100 * fl / (t_at * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2)}
+
+
+def wl_c5(args) -> dict:
+    import torch
+
+    from vllm_apple_amd import kernels, workloads
+
+    dev = torch.device("cuda:0")
+    b = workloads.c5_mixed(device=dev)
+    nd = b.num_decode_tokens
+    T = b.query.shape[0]
+    out = torch.empty_like(b.query)
+    lens = b.extra["seq_lens_host"]
+
+    def attn_step():
+        kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache, b.slot_mapping)
+        kernels.paged_decode(b.query[:nd], b.k_cache, b.v_cache, b.block_table[:nd],
+                             b.seq_lens[:nd], scale=b.scale, max_seq_len=max(lens[:nd]),
+                             output=out[:nd], seq_lens_host=lens[:nd])
+        kernels.paged_prefill(b.query[nd:], b.k_cache, b.v_cache, b.block_table,
+                              b.token_to_seq[nd:], b.positions[nd:], scale=b.scale,
+                              output=out[nd:])
+
+    t_attn = _timed(attn_step, args.steps, args.warmup)
+    x, w = b.extra["hidden"], b.extra["norm_weight"]
+    y = torch.empty_like(x)
+    t_norm = _timed(lambda: kernels.rms_norm(x, w, b.extra["eps"], out=y), args.steps, args.warmup)
+    cos, sin = kernels.rope_cos_sin_cache(b.head_size, 16384, b.extra["rope_base"], device=dev)
+    q2, k2 = b.query.clone(), b.new_k.clone()
+    t_rope = _timed(lambda: kernels.rope_neox_(q2, k2, cos, sin, b.positions), args.steps,
+                    args.warmup)
+    g, u = b.extra["gate"], b.extra["up"]
+    act = torch.empty_like(g)
+    t_silu = _timed(lambda: kernels.silu_mul(g, u, out=act), args.steps, args.warmup)
+    H, KV, D = b.num_q_heads, b.num_kv_heads, b.head_size
+    norm_bytes = 2 * x.numel() * 2 + w.numel() * 2
+    rope_bytes = 2 * (q2.numel() + k2.numel()) * 2 + T * (D // 2) * 4 * 2 + T * 4
+    silu_bytes = 3 * g.numel() * 2
+    kv_read = sum(lens[:nd]) * KV * D * 4
+    pre_ctx = (b.positions[nd:].double() + 1).sum().item()
+    rec = {"workload": "C5", "note": "56 decodes + 8 x 256-token chunks; layer ops over 2104 tokens",
+           "attention_step_ms": round(t_attn, 5),
+           "attention_decode_kv_bytes": kv_read,
+           "attention_prefill_flops": 4.0 * D * H * pre_ctx}
+    for nm, t, by in (("rmsnorm", t_norm, norm_bytes), ("rope", t_rope, rope_bytes),
+                      ("silu_mul", t_silu, silu_bytes)):
+        rec[nm] = {"ms": round(t, 5), "bytes": by, "gb_s": round(by / (t * 1e-3) / 1e9, 1),
+                   "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+    return rec
+
+
+WORKLOADS = {"C1": wl_c1, "C2u": wl_c2u, "C3": wl_c3, "C4": wl_c4, "C5": wl_c5}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -144,6 +310,11 @@ def main() -> int:
     from vllm_apple_amd import _lib, kernels, workloads
 
     _lib.load()
+    if args.workload != "headline":
+        names = ["C1", "C2u", "C3", "C4", "C5"] if args.workload == "all" else [args.workload]
+        for name in names:
+            print(json.dumps(WORKLOADS[name](args)), flush=True)
+        return 0
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     b = workloads.c2_decode(device=dev, fixed_len=args.ctx, batch=args.batch)

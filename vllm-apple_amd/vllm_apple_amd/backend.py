@@ -270,11 +270,14 @@ class HipAttentionImpl(AttentionImpl):
                                        attn_metadata.slot_mapping[:n], layout="vllm")
             nd = attn_metadata.num_decode_tokens
             if nd > 0:
+                # Host lengths, only if already cached (never a device sync here).
+                lens_host = attn_metadata._seq_lens_cpu
                 kernels.paged_decode(query[:nd], key_cache, value_cache,
                                      attn_metadata.block_table[:nd],
                                      attn_metadata.seq_lens[:nd], scale=self.scale,
                                      max_seq_len=attn_metadata.max_seq_len, layout="vllm",
-                                     output=output[:nd])
+                                     output=output[:nd],
+                                     seq_lens_host=lens_host[:nd] if lens_host else None)
             if n > nd:
                 tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,
                                                      attn_metadata.seq_lens, n)

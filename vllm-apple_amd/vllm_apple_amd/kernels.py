@@ -219,18 +219,76 @@ def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
     return int(n), int(part.value)
 
 
+# Decode launch geometry (paged_decode.hip): one workgroup of 8 waves per CU
+# at a time, partitions in multiples of 128 tokens.
+_DECODE_QUANTUM = 128
+_num_cus: dict[int, int] = {}
+
+
+def device_cus(device: torch.device | None = None) -> int:
+    idx = _dev_index(device) if device is not None else torch.cuda.current_device()
+    if idx not in _num_cus:
+        _num_cus[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _num_cus[idx]
+
+
+def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
+                          merge_tokens: int = 256, wg_tokens: int = 96) -> int:
+    """Split-K partition (tokens) for known sequence lengths.
+
+    Estimates the step time in "tokens of one kv head streamed by one CU" for
+    each candidate P: the list-scheduling makespan max(total/m, largest piece)
+    plus half a piece of tail when there is more than one wave of workgroups,
+    a fixed workgroup start-up cost and, when any sequence is split, the merge
+    launch.  Equal lengths that already cover the CUs are left unsplit.
+    Memoised per length tuple (the same step is decoded by every layer).
+    """
+    key = (tuple(int(x) for x in seq_lens_host), int(num_kv_heads), int(num_cus),
+           merge_tokens, wg_tokens)
+    hit = _partition_cache.get(key)
+    if hit is not None:
+        return hit
+    import numpy as np
+
+    lens = np.maximum(np.asarray(key[0], dtype=np.int64), 0)
+    if lens.size == 0 or lens.max() == 0:
+        return 0
+    m = max(1, num_cus)
+    q = _DECODE_QUANTUM
+    longest = int(lens.max())
+    total = float(lens.sum()) * num_kv_heads
+    cands = {((longest + k - 1) // k + q - 1) // q * q for k in range(1, 65)}
+    cands |= {q << i for i in range(0, 10)}
+    P = np.array(sorted(cands), dtype=np.int64)
+    pieces = ((lens[None, :] + P[:, None] - 1) // P[:, None]).sum(axis=1)
+    wgs = pieces * num_kv_heads
+    big = np.minimum(P, longest).astype(np.float64)
+    t = np.maximum(total / m, big) + np.where(wgs > m, big / 2, 0.0) + wg_tokens * wgs / m
+    t = t + np.where(longest > P, merge_tokens, 0)
+    best = int(P[int(np.argmin(t))])
+    if len(_partition_cache) > 4096:
+        _partition_cache.clear()
+    _partition_cache[key] = best
+    return best
+
+
+_partition_cache: dict = {}
+
+
 def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                  block_table: torch.Tensor, seq_lens: torch.Tensor, *, scale: float,
                  max_seq_len: int, layout: str = "kernel", output: torch.Tensor | None = None,
                  new_keys: torch.Tensor | None = None, new_values: torch.Tensor | None = None,
                  partition_size: int = 0, workspace: torch.Tensor | None = None,
-                 stream=None) -> torch.Tensor:
+                 seq_lens_host=None, stream=None) -> torch.Tensor:
     """Paged GQA decode attention, one query token per sequence.
 
     query [num_seqs, H, D] fp16; returns/fills output [num_seqs, H, D].  With
     new_keys/new_values ([num_seqs, KV, D]) the token at position
     seq_lens[s]-1 is written to the cache by the same launch (fused KV write).
-    max_seq_len must bound seq_lens (it sizes the split-K grid).
+    max_seq_len must bound seq_lens (it sizes the split-K grid).  With
+    seq_lens_host (host copies of the lengths, no device sync needed) and
+    partition_size 0 the split-K partition is chosen from the actual lengths.
     """
     _require_gpu(query, key_cache, value_cache, block_table, seq_lens, output, new_keys, new_values)
     _require_dtype(query, torch.float16, "query")
@@ -244,6 +302,9 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
         raise ValueError("new_keys and new_values go together")
     if new_keys is not None and new_keys.stride() != new_values.stride():
         raise ValueError("new_keys and new_values must share strides")
+    if partition_size == 0 and seq_lens_host is not None:
+        kvh = key_cache.shape[1] if layout == "kernel" else key_cache.shape[2]
+        partition_size = choose_partition_size(seq_lens_host, kvh, device_cus(query.device))
     p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
                     num_query_heads=query.shape[1], scale=scale, num_seqs=num_seqs,
                     max_seq_len=max_seq_len, max_blocks_per_seq=block_table.shape[1],
