@@ -57,7 +57,7 @@ def test_prefill_single_seq_with_prefix(gpu):
 
 
 @pytest.mark.parametrize("D", [32, 64, 96, 128])
-@pytest.mark.parametrize("H,KV", [(14, 2), (32, 8), (8, 8), (16, 1)])
+@pytest.mark.parametrize("H,KV", [(14, 2), (32, 8), (8, 8), (16, 1), (6, 2), (8, 4)])
 def test_prefill_shapes(gpu, D, H, KV):
     print(f"[case] prefill D={D} H={H} KV={KV}", flush=True)
     kc, vc, bt, tok, pos, q = _prefill_case([77, 150, 40], [40, 64, 40], H, KV, D, seed=2)
@@ -74,6 +74,14 @@ def test_prefill_c3_shape_subset(gpu, layout):
     rows = torch.randperm(2048, generator=g)[:96].numpy()
     out, ref, w = _run(kc, vc, bt, tok, pos, q, layout=layout, rows=rows)
     assert_close(out[rows], ref[rows], what=f"C3 rows {layout}")
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_prefill_larger_block_size(gpu, bs):
+    kc, vc, bt, tok, pos, q = _prefill_case([300, 77], [120, 77], 32, 8, 128, bs=bs, seed=11)
+    out, ref, w = _run(kc, vc, bt, tok, pos, q)
+    assert w.all()
+    assert_close(out, ref, what=f"prefill bs={bs}")
 
 
 def test_prefill_no_prefix_is_causal_chunk(gpu):

@@ -8,10 +8,11 @@
 // kernel needs no query_start_loc and accepts any token order.
 //
 // Work decomposition
-//   grid  = (32-token query tile, kv_head x head-chunk); a workgroup has one
-//           wave per query head (up to 4 heads of the GQA group), and the
-//           waves share every K/V tile staged in LDS.
-//   For each distinct sequence among the tile's tokens (normally one), the
+//   block = 4 waves = (token subtile, query head) pairs of one kv head: 4 heads
+//           x 32 tokens for GQA groups >= 4, 2 x 64 for pairs, 1 x 128 for MHA.
+//           All waves share every K/V tile staged in LDS.
+//   grid  = (query tile, kv_head x head chunk).
+//   For each distinct sequence among the tile's tokens (normally one) the
 //   workgroup walks 32-key tiles of that sequence's cache:
 //     S^T[32 keys x 32 queries] = K Q^T   (D/16 x mfma 32x32x16)
 //     P = exp2(S*scale*log2e - m), causal/row mask as -inf
@@ -19,14 +20,24 @@
 //   The MFMA output layout of S^T (lane = query, 16 keys per lane) is the B
 //   operand layout of the PV product, so the per-query softmax statistics sit
 //   in the lanes that own the query's accumulators.
+// Memory: K/V tiles are double-buffered in LDS (padded rows of D+8 halves) and
+// filled from registers that were loaded from HBM during the previous tile's
+// math, so one barrier per tile separates load and use.  V^T operands come
+// from LDS with the gfx950 transpose read (ds_read_b64_tr_b16): within each
+// 16-lane group, lanes 4r..4r+3 name 8-byte pieces of row r and lane i
+// receives element i of rows 0..3, which is exactly a 4-key column of V.
 #include "common.h"
 
 namespace vaa {
 namespace {
 
-constexpr int kQT = 32;        // query tokens per workgroup
-constexpr int kKT = 32;        // keys per tile
-constexpr int kMaxWaves = 4;   // query heads per workgroup
+constexpr int kQT = 32;       // query tokens per wave (MFMA columns)
+constexpr int kKT = 32;       // keys per tile
+constexpr int kWavesP = 4;    // waves per workgroup
+constexpr int kXcds = 8;      // accelerator complex dies on MI355X
+constexpr int kThreadsP = kWavesP * kWave;
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const f16* q;
@@ -37,7 +48,9 @@ struct PrefillArgs {
   const int32_t* pos;
   f16* out;
   float scale_log2;
-  int num_tokens, num_seqs, max_blocks, block_size, G, head_chunks;
+  int num_tokens, num_seqs, max_blocks, block_size, G;
+  int heads_per_wg, subtiles, head_chunks;
+  int tiles_y, padded_tiles;  // logical grid rows; workgroups in use (multiple of 8)
   int64_t num_blocks;
   int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
   int64_t q_st, q_sh, o_st, o_sh;
@@ -45,10 +58,12 @@ struct PrefillArgs {
 
 template <int D>
 struct PCfg {
-  static constexpr int LD = D + 8;        // padded LDS row (halves)
-  static constexpr int CH = D / 8;        // 16-byte chunks per row
-  static constexpr int NK = D / 16;       // QK mfma count (K-dim 16)
-  static constexpr int NDT = D / 32;      // PV output tiles of 32 dims
+  static constexpr int LD = D + 8;                      // padded LDS row (halves)
+  static constexpr int CH = D / 8;                      // 16-byte chunks per row
+  static constexpr int NK = D / 16;                     // QK mfma count (K-dim 16)
+  static constexpr int NDT = D / 32;                    // PV output tiles of 32 dims
+  static constexpr int TILE = kKT * LD;                 // halves per staged tile
+  static constexpr int MAXC = (kKT * CH + kThreadsP - 1) / kThreadsP;  // chunks/thread
 };
 
 __device__ __forceinline__ int wave_min_i(int v) {
@@ -62,26 +77,97 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return v;
 }
 
+__device__ __forceinline__ f16x4 lds_tr4(const f16* p) {
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(f16x4, r);
+}
+
+__device__ __forceinline__ bool block_ok(const PrefillArgs& a, const int32_t* bts, int bi) {
+  if (bi >= a.max_blocks) return false;
+  const int64_t phys = bts[bi];
+  return phys >= 0 && phys < a.num_blocks;
+}
+
+// Registers holding this thread's share of one K/V tile on its way to LDS.
 template <int D>
-__global__ void __launch_bounds__(kMaxWaves* kWave)
+struct Stage {
+  u32x4 k[PCfg<D>::MAXC];
+  u32x4 v[PCfg<D>::MAXC];
+};
+
+template <int D>
+__device__ __forceinline__ void stage_load(const PrefillArgs& a, const int32_t* bts, int kvh,
+                                           int key0, int kv_len, Stage<D>& st) {
+  using C = PCfg<D>;
+#pragma unroll
+  for (int i = 0; i < C::MAXC; ++i) {
+    const int f = threadIdx.x + i * kThreadsP;
+    st.k[i] = u32x4{0u, 0u, 0u, 0u};
+    st.v[i] = u32x4{0u, 0u, 0u, 0u};
+    if (f < kKT * C::CH) {
+      const int kr = f / C::CH, ch = f % C::CH;
+      const int kpos = key0 + kr;
+      if (kpos < kv_len) {
+        const int bi = kpos / a.block_size;
+        const int64_t phys = bi < a.max_blocks ? bts[bi] : -1;
+        if (phys >= 0 && phys < a.num_blocks) {
+          const int row = kpos - bi * a.block_size;
+          st.k[i] = ld16(a.kc + phys * a.k_sb + kvh * a.k_sh + row * a.k_st + ch * 8);
+          st.v[i] = ld16(a.vc + phys * a.v_sb + kvh * a.v_sh + row * a.v_st + ch * 8);
+        }
+      }
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store(f16* ks, f16* vs, const Stage<D>& st) {
+  using C = PCfg<D>;
+#pragma unroll
+  for (int i = 0; i < C::MAXC; ++i) {
+    const int f = threadIdx.x + i * kThreadsP;
+    if (f < kKT * C::CH) {
+      const int kr = f / C::CH, ch = f % C::CH;
+      *reinterpret_cast<u32x4*>(ks + kr * C::LD + ch * 8) = st.k[i];
+      *reinterpret_cast<u32x4*>(vs + kr * C::LD + ch * 8) = st.v[i];
+    }
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(kThreadsP)
 paged_prefill_kernel(PrefillArgs a) {
   using C = PCfg<D>;
-  __shared__ __align__(16) f16 ks[kKT * C::LD];
-  __shared__ __align__(16) f16 vs[kKT * C::LD];
-  __shared__ int s_bad;  // bit b set: 16-key sub-block b of the tile is invalid
+  __shared__ __align__(16) f16 ks[2][C::TILE];
+  __shared__ __align__(16) f16 vs[2][C::TILE];
+  __shared__ int red[2][kWavesP];
 
-  const int tile0 = blockIdx.x * kQT;
-  const int kvh = blockIdx.y / a.head_chunks;
-  const int hchunk = blockIdx.y % a.head_chunks;
+  // XCD-aware placement: the hardware hands consecutive workgroup ids to the
+  // 8 XCDs in turn, so id i runs on XCD i % 8.  Give each XCD a contiguous
+  // range of (kv head, query tile) work so the query tiles that reuse one
+  // sequence's K/V tiles share that XCD's L2.
+  const int gx = gridDim.x;
+  const int id = blockIdx.x + gx * blockIdx.y;
+  if (id >= a.padded_tiles) return;  // grid rounding beyond the padded count
+  const int per_xcd = a.padded_tiles / kXcds;
+  const int logical = (id % kXcds) * per_xcd + id / kXcds;
+  if (logical >= gx * a.tiles_y) return;
+  const int tile_x = logical % gx, tile_y = logical / gx;
+  const int kvh = tile_y / a.head_chunks;
+  const int hchunk = tile_y % a.head_chunks;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int nthreads = blockDim.x;
-  const int head = kvh * a.G + hchunk * kMaxWaves + wave;  // query head
+  const int hw = wave % a.heads_per_wg, sub = wave / a.heads_per_wg;
+  const int ghead = hchunk * a.heads_per_wg + hw;             // head index in the group
+  const bool math = sub < a.subtiles && ghead < a.G;         // this wave computes
+  const int head = kvh * a.G + (ghead < a.G ? ghead : 0);
   const int qj = lane & 31, hb = lane >> 5;
+  const int g16 = lane >> 4, i16 = lane & 15;
 
   // Per-lane query token (lanes l and l+32 share token qj).
-  const int tok = tile0 + qj;
+  const int tok = tile_x * (kQT * a.subtiles) + (sub < a.subtiles ? sub : 0) * kQT + qj;
   int tseq = -1, tpos = -1;
-  if (tok < a.num_tokens) {
+  if (sub < a.subtiles && tok < a.num_tokens) {
     tseq = a.tok_seq[tok];
     tpos = a.pos[tok];
   }
@@ -96,7 +182,7 @@ paged_prefill_kernel(PrefillArgs a) {
   // Q^T as B operand: lane holds Q[token qj][hb*D/2 + 8s .. +7], s < NK.
   u32x4 qb[C::NK];
   {
-    const bool ld = row_ok && head < kvh * a.G + a.G;
+    const bool ld = row_ok && math;
     const f16* qp = a.q + static_cast<int64_t>(ld ? tok : 0) * a.q_st + head * a.q_sh +
                     hb * (D / 2);
 #pragma unroll
@@ -110,108 +196,107 @@ paged_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
+  // LDS element offsets of this lane's operand reads (constant over tiles).
+  const int k_rd = qj * C::LD + hb * (D / 2);
+  const int v_rd = (4 * hb + (i16 >> 2)) * C::LD + 16 * (g16 & 1) + 4 * (i16 & 3);
+
   while (true) {
-    const int cand = done ? INT32_MAX : tseq;
-    const int s = wave_min_i(cand);
-    if (s == INT32_MAX) break;  // identical in every wave: same tokens
+    // Next sequence among the workgroup's unfinished tokens, and its context.
+    int s = wave_min_i(done ? INT32_MAX : tseq);
+    if (lane == 0) red[0][wave] = s;
+    __syncthreads();
+    s = red[0][0];
+#pragma unroll
+    for (int w = 1; w < kWavesP; ++w) s = min(s, red[0][w]);
+    if (s == INT32_MAX) break;
     const bool active = !done && tseq == s;
-    const int kv_len = wave_max_i(active ? tpos + 1 : 0);
+    int kv_len = wave_max_i(active ? tpos + 1 : 0);
+    if (lane == 0) red[1][wave] = kv_len;
+    __syncthreads();
+    kv_len = red[1][0];
+#pragma unroll
+    for (int w = 1; w < kWavesP; ++w) kv_len = max(kv_len, red[1][w]);
     const int n_kt = (kv_len + kKT - 1) / kKT;
     const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
+    const int lim = active ? tpos : -1;  // last key position this row may see
 
+    Stage<D> st;
+    stage_load<D>(a, bts, kvh, 0, kv_len, st);
+    stage_store<D>(ks[0], vs[0], st);
+    __syncthreads();
     for (int kt = 0; kt < n_kt; ++kt) {
       const int key0 = kt * kKT;
-      __syncthreads();  // previous tile fully consumed
-      if (threadIdx.x == 0) s_bad = 0;
-      __syncthreads();
-      // Stage K and V rows [key0, key0+32) of sequence s into LDS.
-      for (int f = threadIdx.x; f < kKT * C::CH; f += nthreads) {
-        const int kr = f / C::CH, ch = f % C::CH;
-        const int kpos = key0 + kr;
-        const int bi = kpos / a.block_size;
-        int64_t phys = bi < a.max_blocks ? bts[bi] : -1;
-        const bool bvalid = phys >= 0 && phys < a.num_blocks;
-        u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-        if (bvalid && kpos < kv_len) {
-          const int row = kpos - bi * a.block_size;
-          kv = ld16(a.kc + phys * a.k_sb + kvh * a.k_sh + row * a.k_st + ch * 8);
-          vv = ld16(a.vc + phys * a.v_sb + kvh * a.v_sh + row * a.v_st + ch * 8);
-        }
-        if (!bvalid && kpos < kv_len && ch == 0) atomicOr(&s_bad, 1 << (kr / 16));
-        *reinterpret_cast<u32x4*>(ks + kr * C::LD + ch * 8) = kv;
-        *reinterpret_cast<u32x4*>(vs + kr * C::LD + ch * 8) = vv;
-      }
-      __syncthreads();
+      const int buf = kt & 1;
+      if (kt + 1 < n_kt) stage_load<D>(a, bts, kvh, key0 + kKT, kv_len, st);
+
       // A row aborts (is never written) when a block inside its context is
       // invalid, as paged_attention_v2.metal:428 does.
-      const int bad = s_bad;
-      if (active && bad) {
-        for (int b = 0; b < 2; ++b)
-          if ((bad >> b) & 1)
-            if (key0 + 16 * b <= tpos) aborted = true;
-      }
-      if (head >= kvh * a.G + a.G) continue;  // idle wave (G not a multiple of 4)
+      if (!block_ok(a, bts, key0 / a.block_size) && key0 <= lim) aborted = true;
+      if (key0 + 16 < kv_len && !block_ok(a, bts, (key0 + 16) / a.block_size) &&
+          key0 + 16 <= lim)
+        aborted = true;
 
-      // S^T = K Q^T : A lane = K[key l%32][hb*D/2 + 8s .. +7].
-      f32x16 st;
+      if (math) {
+        const f16* kb = ks[buf];
+        const f16* vb = vs[buf];
+        // S^T = K Q^T : A lane = K[key l%32][hb*D/2 + 8s .. +7].
+        f32x16 sacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st[r] = 0.f;
-      const f16* krow = ks + qj * C::LD + hb * (D / 2);
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
 #pragma unroll
-      for (int s2 = 0; s2 < C::NK; ++s2) {
-        const u32x4 kA = *reinterpret_cast<const u32x4*>(krow + 8 * s2);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
-                                                    __builtin_bit_cast(f16x8, qb[s2]),
-                                                    st, 0, 0, 0);
-      }
-      // Lane holds keys 8(r/4) + 4hb + r%4 for query qj.
-      float x[16];
-      float mx = -INFINITY;
+        for (int s2 = 0; s2 < C::NK; ++s2) {
+          const u32x4 kA = *reinterpret_cast<const u32x4*>(kb + k_rd + 8 * s2);
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
+                                                        __builtin_bit_cast(f16x8, qb[s2]),
+                                                        sacc, 0, 0, 0);
+        }
+        // Lane holds keys 8(r/4) + 4hb + r%4 for query qj.
+        float x[16];
+        float mx = -INFINITY;
+        const int rel = lim - key0;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kp = key0 + 8 * (r >> 2) + 4 * hb + (r & 3);
-        const bool ok = active && kp <= tpos;
-        x[r] = ok ? st[r] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, x[r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
-      const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;
-      f16x8 pb[2];
-      float psum = 0.f;
+        for (int r = 0; r < 16; ++r) {
+          const int kl = 8 * (r >> 2) + 4 * hb + (r & 3);
+          x[r] = kl <= rel ? sacc[r] * a.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, x[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(m_run, mx);
+        if (m_new != m_run) {
+          const float alpha = fast_exp2(m_run - m_new);  // 0 when m_run = -inf
+          l_part *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const f16 p = f2h(fast_exp2(x[r] - m_sub));
-        pb[r >> 3][r & 7] = p;
-        psum += h2f(p);
-      }
-      l_part = l_part * alpha + psum;
-      m_run = m_new;
-      if (alpha != 1.f) {
+          for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
+          m_run = m_new;
+        }
+        const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
+        f16x8 pb[2];
 #pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
-      }
-      // O^T += V^T P^T. MFMA c covers keys 16c + 4hb + (i%4) + 8(i/4), i < 8.
+        for (int r = 0; r < 16; ++r) {
+          const f16 p = f2h(fast_exp2(x[r] - m_sub));
+          pb[r >> 3][r & 7] = p;
+          l_part += h2f(p);
+        }
+        // O^T += V^T P^T; MFMA c covers keys 16c + 4hb + (i%4) + 8(i/4), i < 8.
 #pragma unroll
-      for (int dt = 0; dt < C::NDT; ++dt) {
-        const int d = 32 * dt + qj;
+        for (int dt = 0; dt < C::NDT; ++dt) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          f16x8 va;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int key = 16 * c + 4 * hb + (i & 3) + 8 * (i >> 2);
-            va[i] = vs[key * C::LD + d];
+          for (int c = 0; c < 2; ++c) {
+            const f16* vp = vb + v_rd + (16 * c) * C::LD + 32 * dt;
+            const f16x4 lo = lds_tr4(vp);
+            const f16x4 hi = lds_tr4(vp + 8 * C::LD);
+            const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], acc[dt], 0, 0, 0);
           }
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], acc[dt], 0, 0, 0);
         }
       }
+      if (kt + 1 < n_kt) stage_store<D>(ks[buf ^ 1], vs[buf ^ 1], st);
+      __syncthreads();
     }
     done = done || active;
   }
 
-  if (head >= kvh * a.G + a.G) return;
+  if (!math) return;
   const float l_tot = l_part + __shfl_xor(l_part, 32, kWave);
   if (!row_ok || aborted) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -231,9 +316,16 @@ paged_prefill_kernel(PrefillArgs a) {
 
 template <int D>
 int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
-  const int waves = a.G < kMaxWaves ? a.G : kMaxWaves;
-  dim3 grid((a.num_tokens + kQT - 1) / kQT, num_kv_heads * a.head_chunks);
-  hipLaunchKernelGGL(paged_prefill_kernel<D>, grid, dim3(waves * kWave), 0, stream, a);
+  const int per_wg = kQT * a.subtiles;
+  const int gx = (a.num_tokens + per_wg - 1) / per_wg, gy = num_kv_heads * a.head_chunks;
+  // Pad the grid to a multiple of the XCD count so every logical tile has a
+  // slot under the XCD remap (surplus workgroups exit at once).
+  const int total = gx * gy, padded = (total + kXcds - 1) / kXcds * kXcds;
+  PrefillArgs b = a;
+  b.tiles_y = gy;
+  b.padded_tiles = padded;
+  dim3 grid(gx, (padded + gx - 1) / gx);
+  hipLaunchKernelGGL(paged_prefill_kernel<D>, grid, dim3(kThreadsP), 0, stream, b);
   return check_launch("paged_prefill_kernel");
 }
 
@@ -293,7 +385,16 @@ extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
   a.max_blocks = p->max_blocks_per_seq;
   a.block_size = p->block_size;
   a.G = p->queries_per_kv;
-  a.head_chunks = (a.G + kMaxWaves - 1) / kMaxWaves;
+  // Waves = (token subtile, head) pairs: 4 heads x 32 tokens when the group
+  // has >= 3 heads, 2 x 64 for pairs, 1 x 128 for MHA.
+  if (a.G >= 3) {
+    a.heads_per_wg = a.G >= 4 ? 4 : 3;
+    a.subtiles = 1;
+  } else {
+    a.heads_per_wg = a.G;
+    a.subtiles = kWavesP / a.G;
+  }
+  a.head_chunks = (a.G + a.heads_per_wg - 1) / a.heads_per_wg;
   a.num_blocks = p->num_blocks;
   a.k_sb = p->k_stride_block; a.k_sh = p->k_stride_head; a.k_st = p->k_stride_token;
   a.v_sb = p->v_stride_block; a.v_sh = p->v_stride_head; a.v_st = p->v_stride_token;
