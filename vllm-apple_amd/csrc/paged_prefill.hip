@@ -35,6 +35,7 @@ constexpr int kQT = 32;       // query tokens per wave (MFMA columns)
 constexpr int kKT = 32;       // keys per tile
 constexpr int kWavesP = 4;    // waves per workgroup
 constexpr int kXcds = 8;      // accelerator complex dies on MI355X
+constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 constexpr int kThreadsP = kWavesP * kWave;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -83,12 +84,6 @@ __device__ __forceinline__ f16x4 lds_tr4(const f16* p) {
   return __builtin_bit_cast(f16x4, r);
 }
 
-__device__ __forceinline__ bool block_ok(const PrefillArgs& a, const int32_t* bts, int bi) {
-  if (bi >= a.max_blocks) return false;
-  const int64_t phys = bts[bi];
-  return phys >= 0 && phys < a.num_blocks;
-}
-
 // Registers holding this thread's share of one K/V tile on its way to LDS.
 template <int D>
 struct Stage {
@@ -96,10 +91,58 @@ struct Stage {
   u32x4 v[PCfg<D>::MAXC];
 };
 
+// The block-table entries of 64 consecutive blocks sit in one VGPR (one per
+// lane) and are read with readlane, so the tile loop issues no scalar loads
+// whose latency would sit in front of the K/V loads.
+struct BlockWindow {
+  int base;  // first block index held
+  int vals;  // lane i: physical block of block base + i, or -1
+};
+
+__device__ __forceinline__ void window_load(const PrefillArgs& a, const int32_t* bts, int base,
+                                            BlockWindow& w) {
+  const int e = base + static_cast<int>(threadIdx.x % kWave);
+  w.base = base;
+  w.vals = e < a.max_blocks ? bts[e] : -1;
+}
+
+// Physical block of block index bi (wave-uniform), or -1 when the entry is
+// missing or out of range.
+__device__ __forceinline__ int64_t window_block(const PrefillArgs& a, const int32_t* bts,
+                                                int bi, BlockWindow& w) {
+  if (bi >= w.base + kWave) window_load(a, bts, bi, w);
+  const int64_t phys = __builtin_amdgcn_readlane(w.vals, bi - w.base);
+  return (phys >= 0 && phys < a.num_blocks) ? phys : -1;
+}
+
+// Each 16-row half of a 32-key tile lies inside one cache block (block_size
+// is a multiple of 16), so its base address is uniform and every thread adds
+// a constant in-tile offset.  Rows past kv_len and rows of an invalid block
+// are zero-filled.  A row whose context [0, lim] reaches an invalid block
+// aborts (is never written), as paged_attention_v2.metal:428 does.
 template <int D>
 __device__ __forceinline__ void stage_load(const PrefillArgs& a, const int32_t* bts, int kvh,
-                                           int key0, int kv_len, Stage<D>& st) {
+                                           int key0, int kv_len, int lim, BlockWindow& w,
+                                           bool& aborted, Stage<D>& st) {
   using C = PCfg<D>;
+  const f16* kb[2];
+  const f16* vb[2];
+  bool ok[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int k0 = key0 + 16 * h;
+    const int bi = k0 / a.block_size;
+    int64_t phys = -1;
+    if (k0 < kv_len) {
+      phys = window_block(a, bts, bi, w);
+      if (phys < 0 && k0 <= lim) aborted = true;
+    }
+    ok[h] = phys >= 0;
+    if (!ok[h]) phys = 0;
+    const int row0 = k0 - bi * a.block_size;
+    kb[h] = a.kc + phys * a.k_sb + kvh * a.k_sh + row0 * a.k_st;
+    vb[h] = a.vc + phys * a.v_sb + kvh * a.v_sh + row0 * a.v_st;
+  }
 #pragma unroll
   for (int i = 0; i < C::MAXC; ++i) {
     const int f = threadIdx.x + i * kThreadsP;
@@ -107,15 +150,10 @@ __device__ __forceinline__ void stage_load(const PrefillArgs& a, const int32_t* 
     st.v[i] = u32x4{0u, 0u, 0u, 0u};
     if (f < kKT * C::CH) {
       const int kr = f / C::CH, ch = f % C::CH;
-      const int kpos = key0 + kr;
-      if (kpos < kv_len) {
-        const int bi = kpos / a.block_size;
-        const int64_t phys = bi < a.max_blocks ? bts[bi] : -1;
-        if (phys >= 0 && phys < a.num_blocks) {
-          const int row = kpos - bi * a.block_size;
-          st.k[i] = ld16(a.kc + phys * a.k_sb + kvh * a.k_sh + row * a.k_st + ch * 8);
-          st.v[i] = ld16(a.vc + phys * a.v_sb + kvh * a.v_sh + row * a.v_st + ch * 8);
-        }
+      const int h = kr >> 4, r = kr & 15;
+      if (ok[h] && key0 + kr < kv_len) {
+        st.k[i] = ld16(kb[h] + r * a.k_st + ch * 8);
+        st.v[i] = ld16(vb[h] + r * a.v_st + ch * 8);
       }
     }
   }
@@ -135,8 +173,75 @@ __device__ __forceinline__ void stage_store(f16* ks, f16* vs, const Stage<D>& st
   }
 }
 
+// One 32-key tile for this wave's 32 query rows: S^T = K Q^T, online
+// softmax, O^T += V^T P^T.
 template <int D>
-__global__ void __launch_bounds__(kThreadsP)
+__device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kb, const f16* vb,
+                                          int key0, int lim, int k_rd, int v_rd, int hb,
+                                          const u32x4 (&qb)[PCfg<D>::NK], float& m_run,
+                                          float& l_part, f32x16 (&acc)[PCfg<D>::NDT]) {
+  using C = PCfg<D>;
+  // S^T = K Q^T : A lane = K[key l%32][hb*D/2 + 8s .. +7].
+  f32x16 sacc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < C::NK; ++s2) {
+    const u32x4 kA = *reinterpret_cast<const u32x4*>(kb + k_rd + 8 * s2);
+    sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
+                                                  __builtin_bit_cast(f16x8, qb[s2]), sacc, 0,
+                                                  0, 0);
+  }
+  // Lane holds keys 8(r/4) + 4hb + r%4 for query qj.  The mask is only
+  // evaluated when some row of the wave cannot see the whole tile.
+  const int rel = lim - key0;
+  float mx = -INFINITY;
+  if (__builtin_amdgcn_ballot_w64(rel < kKT - 1) != 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kl = 8 * (r >> 2) + 4 * hb + (r & 3);
+      if (kl > rel) sacc[r] = -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;
+  // Lazy rescale: keep the reference max unless a score exceeds it by more
+  // than 2^8 (p stays <= 256, exact in fp16); the wave-uniform branch is
+  // taken on a row's first tile and on rare outliers only.  Only lanes whose
+  // max grows rescale (a fully masked lane keeps m_run = -inf and must not
+  // form -inf - -inf).
+  if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0 && mx > m_run) {
+    const float alpha = fast_exp2(m_run - mx);  // 0 when m_run = -inf
+    l_part *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
+    m_run = mx;
+  }
+  const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
+  f16x8 pb[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float p = fast_exp2(fmaf(sacc[r], a.scale_log2, -m_sub));
+    pb[r >> 3][r & 7] = f2h(p);
+    l_part += p;
+  }
+  // O^T += V^T P^T; MFMA c covers keys 16c + 4hb + (i%4) + 8(i/4), i < 8.
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const f16* vp = vb + v_rd + (16 * c) * C::LD + 32 * dt;
+      const f16x4 lo = lds_tr4(vp);
+      const f16x4 hi = lds_tr4(vp + 8 * C::LD);
+      const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], acc[dt], 0, 0, 0);
+    }
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(kThreadsP) __attribute__((amdgpu_waves_per_eu(2, 2)))
 paged_prefill_kernel(PrefillArgs a) {
   using C = PCfg<D>;
   __shared__ __align__(16) f16 ks[2][C::TILE];
@@ -220,77 +325,25 @@ paged_prefill_kernel(PrefillArgs a) {
     const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
     const int lim = active ? tpos : -1;  // last key position this row may see
 
-    Stage<D> st;
-    stage_load<D>(a, bts, kvh, 0, kv_len, st);
-    stage_store<D>(ks[0], vs[0], st);
+    // Two register stages rotate so K/V loads run two tiles ahead of the
+    // math; LDS holds the tile being computed and the next one.
+    BlockWindow win;
+    window_load(a, bts, 0, win);
+    Stage<D> sa, sb;
+    stage_load<D>(a, bts, kvh, 0, kv_len, lim, win, aborted, sa);
+    if (n_kt > 1) stage_load<D>(a, bts, kvh, kKT, kv_len, lim, win, aborted, sb);
+    stage_store<D>(ks[0], vs[0], sa);
     __syncthreads();
-    for (int kt = 0; kt < n_kt; ++kt) {
-      const int key0 = kt * kKT;
-      const int buf = kt & 1;
-      if (kt + 1 < n_kt) stage_load<D>(a, bts, kvh, key0 + kKT, kv_len, st);
-
-      // A row aborts (is never written) when a block inside its context is
-      // invalid, as paged_attention_v2.metal:428 does.
-      if (!block_ok(a, bts, key0 / a.block_size) && key0 <= lim) aborted = true;
-      if (key0 + 16 < kv_len && !block_ok(a, bts, (key0 + 16) / a.block_size) &&
-          key0 + 16 <= lim)
-        aborted = true;
-
-      if (math) {
-        const f16* kb = ks[buf];
-        const f16* vb = vs[buf];
-        // S^T = K Q^T : A lane = K[key l%32][hb*D/2 + 8s .. +7].
-        f32x16 sacc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
-#pragma unroll
-        for (int s2 = 0; s2 < C::NK; ++s2) {
-          const u32x4 kA = *reinterpret_cast<const u32x4*>(kb + k_rd + 8 * s2);
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
-                                                        __builtin_bit_cast(f16x8, qb[s2]),
-                                                        sacc, 0, 0, 0);
-        }
-        // Lane holds keys 8(r/4) + 4hb + r%4 for query qj.
-        float x[16];
-        float mx = -INFINITY;
-        const int rel = lim - key0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kl = 8 * (r >> 2) + 4 * hb + (r & 3);
-          x[r] = kl <= rel ? sacc[r] * a.scale_log2 : -INFINITY;
-          mx = fmaxf(mx, x[r]);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float m_new = fmaxf(m_run, mx);
-        if (m_new != m_run) {
-          const float alpha = fast_exp2(m_run - m_new);  // 0 when m_run = -inf
-          l_part *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
-          m_run = m_new;
-        }
-        const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
-        f16x8 pb[2];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const f16 p = f2h(fast_exp2(x[r] - m_sub));
-          pb[r >> 3][r & 7] = p;
-          l_part += h2f(p);
-        }
-        // O^T += V^T P^T; MFMA c covers keys 16c + 4hb + (i%4) + 8(i/4), i < 8.
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) {
-#pragma unroll
-          for (int c = 0; c < 2; ++c) {
-            const f16* vp = vb + v_rd + (16 * c) * C::LD + 32 * dt;
-            const f16x4 lo = lds_tr4(vp);
-            const f16x4 hi = lds_tr4(vp + 8 * C::LD);
-            const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], acc[dt], 0, 0, 0);
-          }
-        }
-      }
-      if (kt + 1 < n_kt) stage_store<D>(ks[buf ^ 1], vs[buf ^ 1], st);
+    for (int kt = 0; kt < n_kt; kt += 2) {
+      if (kt + 2 < n_kt) stage_load<D>(a, bts, kvh, (kt + 2) * kKT, kv_len, lim, win, aborted, sa);
+      if (math) tile_math<D>(a, ks[0], vs[0], kt * kKT, lim, k_rd, v_rd, hb, qb, m_run, l_part, acc);
+      if (kt + 1 < n_kt) stage_store<D>(ks[1], vs[1], sb);
+      __syncthreads();
+      if (kt + 1 >= n_kt) break;
+      if (kt + 3 < n_kt) stage_load<D>(a, bts, kvh, (kt + 3) * kKT, kv_len, lim, win, aborted, sb);
+      if (math)
+        tile_math<D>(a, ks[1], vs[1], (kt + 1) * kKT, lim, k_rd, v_rd, hb, qb, m_run, l_part, acc);
+      if (kt + 2 < n_kt) stage_store<D>(ks[0], vs[0], sa);
       __syncthreads();
     }
     done = done || active;
