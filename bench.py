@@ -113,7 +113,7 @@ def cpu_baseline(batch, budget_s: float) -> dict:
     ref_torch.decode_sdpa(q, kc, vc, local_bt, lens, batch.scale, kv)  # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 1000):
         t0 = time.perf_counter()
         ref_torch.decode_sdpa(q, kc, vc, local_bt, lens, batch.scale, kv)
         times.append(time.perf_counter() - t0)
