@@ -13,32 +13,42 @@
 //           All waves share every K/V tile staged in LDS.
 //   grid  = (query tile, kv_head x head chunk).
 //   For each distinct sequence among the tile's tokens (normally one) the
-//   workgroup walks 32-key tiles of that sequence's cache:
-//     S^T[32 keys x 32 queries] = K Q^T   (D/16 x mfma 32x32x16)
+//   workgroup walks 64-key tiles of that sequence's cache:
+//     S^T[64 keys x 32 queries] = K Q^T   (2 x D/16 mfma 32x32x16)
 //     P = exp2(S*scale*log2e - m), causal/row mask as -inf
-//     O^T[D x 32 queries]      += V^T P^T (D/16 x mfma 32x32x16)
+//     O^T[D x 32 queries]      += V^T P^T (D/32 x 4 mfma 32x32x16)
 //   The MFMA output layout of S^T (lane = query, 16 keys per lane) is the B
 //   operand layout of the PV product, so the per-query softmax statistics sit
 //   in the lanes that own the query's accumulators.
-// Memory: K/V tiles are double-buffered in LDS (padded rows of D+8 halves) and
-// filled from registers that were loaded from HBM during the previous tile's
-// math, so one barrier per tile separates load and use.  V^T operands come
-// from LDS with the gfx950 transpose read (ds_read_b64_tr_b16): within each
-// 16-lane group, lanes 4r..4r+3 name 8-byte pieces of row r and lane i
-// receives element i of rows 0..3, which is exactly a 4-key column of V.
+//
+// Memory: K/V tiles move from HBM straight into LDS with the gfx950 direct
+// loads (global_load_lds_dwordx4: lane i of a wave writes LDS bytes
+// [16i, 16i+16) after the wave-uniform base), double-buffered in four
+// distinct LDS arrays so the next tile streams in during this tile's math
+// with no registers, address arithmetic or LDS stores of its own.  Wave w
+// fetches the tile's 16-key group w, which lies inside one cache block.
+// Rows are unpadded; 16-byte chunks are XOR-swizzled by row so that both the
+// K operand reads (ds_read_b128 down 32 rows) and the transposed V^T reads
+// (ds_read_b64_tr_b16: within each 16-lane group, lanes 4r..4r+3 name 8-byte
+// pieces of row r and lane i receives element i of rows 0..3) hit distinct
+// banks.  V rows past the context or in a missing block are zero-filled, so
+// masked keys (P = 0) contribute exactly zero.
 #include "common.h"
 
 namespace vaa {
 namespace {
 
 constexpr int kQT = 32;       // query tokens per wave (MFMA columns)
-constexpr int kKT = 32;       // keys per tile
+constexpr int kKT = 64;       // keys per tile: four 16-key groups, one per wave
 constexpr int kWavesP = 4;    // waves per workgroup
 constexpr int kXcds = 8;      // accelerator complex dies on MI355X
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 constexpr int kThreadsP = kWavesP * kWave;
+static_assert(kKT == 16 * kWavesP, "one 16-key group per wave");
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
 
 struct PrefillArgs {
   const f16* q;
@@ -50,6 +60,7 @@ struct PrefillArgs {
   f16* out;
   float scale_log2;
   int num_tokens, num_seqs, max_blocks, block_size, G;
+  int bs_shift;               // log2(block_size) when it is a power of two, else -1
   int heads_per_wg, subtiles, head_chunks;
   int tiles_y, padded_tiles;  // logical grid rows; workgroups in use (multiple of 8)
   int64_t num_blocks;
@@ -59,13 +70,23 @@ struct PrefillArgs {
 
 template <int D>
 struct PCfg {
-  static constexpr int LD = D + 8;                      // padded LDS row (halves)
-  static constexpr int CH = D / 8;                      // 16-byte chunks per row
-  static constexpr int NK = D / 16;                     // QK mfma count (K-dim 16)
-  static constexpr int NDT = D / 32;                    // PV output tiles of 32 dims
-  static constexpr int TILE = kKT * LD;                 // halves per staged tile
-  static constexpr int MAXC = (kKT * CH + kThreadsP - 1) / kThreadsP;  // chunks/thread
+  static constexpr int CH = D / 8;             // 16-byte chunks per row
+  static constexpr int NK = D / 16;            // QK mfma steps (K-dim 16)
+  static constexpr int NDT = D / 32;           // PV output tiles of 32 dims
+  static constexpr int TILE = kKT * D;         // halves per staged K or V tile
+  static constexpr int NI = CH / 4;            // direct loads per wave per tile (K or V)
+  static constexpr int ROWB = D * 2;           // bytes per LDS row
 };
+
+// Chunk swizzle: physical chunk = logical chunk ^ swz(row).  For 8 or 16
+// chunks per row the XOR takes all 8 values over 8 consecutive rows (K reads
+// conflict-free) and distinct pairs over 4 aligned rows (V^T reads
+// conflict-free); for 4 or 12 chunks it stays inside aligned groups of 4.
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (D == 64 || D == 128) return ((row & 3) << 1) | ((row >> 2) & 1);
+  else return (row >> 1) & 3;
+}
 
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
@@ -84,16 +105,13 @@ __device__ __forceinline__ f16x4 lds_tr4(const f16* p) {
   return __builtin_bit_cast(f16x4, r);
 }
 
-// Registers holding this thread's share of one K/V tile on its way to LDS.
-template <int D>
-struct Stage {
-  u32x4 k[PCfg<D>::MAXC];
-  u32x4 v[PCfg<D>::MAXC];
-};
+// s_waitcnt vmcnt(0) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4 left at its maximum, lgkmcnt 11:8): every direct load and LDS
+// access of this wave has landed.
+__device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
 
 // The block-table entries of 64 consecutive blocks sit in one VGPR (one per
-// lane) and are read with readlane, so the tile loop issues no scalar loads
-// whose latency would sit in front of the K/V loads.
+// lane) and are read with readlane, so the tile loop issues no scalar loads.
 struct BlockWindow {
   int base;  // first block index held
   int vals;  // lane i: physical block of block base + i, or -1
@@ -115,96 +133,140 @@ __device__ __forceinline__ int64_t window_block(const PrefillArgs& a, const int3
   return (phys >= 0 && phys < a.num_blocks) ? phys : -1;
 }
 
-// Each 16-row half of a 32-key tile lies inside one cache block (block_size
-// is a multiple of 16), so its base address is uniform and every thread adds
-// a constant in-tile offset.  Rows past kv_len and rows of an invalid block
-// are zero-filled.  A row whose context [0, lim] reaches an invalid block
-// aborts (is never written), as paged_attention_v2.metal:428 does.
+// Loop-invariant per-lane addressing.
 template <int D>
-__device__ __forceinline__ void stage_load(const PrefillArgs& a, const int32_t* bts, int kvh,
-                                           int key0, int kv_len, int lim, BlockWindow& w,
-                                           bool& aborted, Stage<D>& st) {
+struct Lanes {
+  uint32_t koff[PCfg<D>::NI];  // byte offset of this lane's chunk inside its K group
+  uint32_t voff[PCfg<D>::NI];
+  int row[PCfg<D>::NI];        // row inside the 16-key group for each direct load
+  int kaddr[PCfg<D>::NK];      // LDS byte address of the K operand for step s
+  int vaddr[PCfg<D>::NDT];     // LDS byte address of the V^T operand for dim tile dt
+};
+
+template <int D>
+__device__ __forceinline__ void lanes_init(const PrefillArgs& a, int wave, int lane,
+                                           Lanes<D>& L) {
   using C = PCfg<D>;
-  const f16* kb[2];
-  const f16* vb[2];
-  bool ok[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int k0 = key0 + 16 * h;
-    const int bi = k0 / a.block_size;
-    int64_t phys = -1;
-    if (k0 < kv_len) {
-      phys = window_block(a, bts, bi, w);
-      if (phys < 0 && k0 <= lim) aborted = true;
-    }
-    ok[h] = phys >= 0;
-    if (!ok[h]) phys = 0;
-    const int row0 = k0 - bi * a.block_size;
-    kb[h] = a.kc + phys * a.k_sb + kvh * a.k_sh + row0 * a.k_st;
-    vb[h] = a.vc + phys * a.v_sb + kvh * a.v_sh + row0 * a.v_st;
+  for (int q = 0; q < C::NI; ++q) {
+    const int P = 64 * (wave * C::NI + q) + lane;  // chunk slot in the tile
+    const int R = P / C::CH;                         // tile row (16*wave .. +15)
+    const int lc = (P % C::CH) ^ swz<D>(R);          // logical chunk stored there
+    L.row[q] = R & 15;
+    L.koff[q] = static_cast<uint32_t>((R & 15) * a.k_st * 2 + lc * 16);
+    L.voff[q] = static_cast<uint32_t>((R & 15) * a.v_st * 2 + lc * 16);
   }
+  const int qj = lane & 31, hb = lane >> 5;
+  const int sk = swz<D>(qj);
 #pragma unroll
-  for (int i = 0; i < C::MAXC; ++i) {
-    const int f = threadIdx.x + i * kThreadsP;
-    st.k[i] = u32x4{0u, 0u, 0u, 0u};
-    st.v[i] = u32x4{0u, 0u, 0u, 0u};
-    if (f < kKT * C::CH) {
-      const int kr = f / C::CH, ch = f % C::CH;
-      const int h = kr >> 4, r = kr & 15;
-      if (ok[h] && key0 + kr < kv_len) {
-        st.k[i] = ld16(kb[h] + r * a.k_st + ch * 8);
-        st.v[i] = ld16(vb[h] + r * a.v_st + ch * 8);
+  for (int s2 = 0; s2 < C::NK; ++s2)
+    L.kaddr[s2] = qj * C::ROWB + ((hb * (C::CH / 2) + s2) ^ sk) * 16;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int r = 4 * hb + (i16 >> 2), j4 = i16 & 3;
+  const int sv = swz<D>(r);
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt)
+    L.vaddr[dt] = r * C::ROWB + ((4 * dt + 2 * (g16 & 1) + (j4 >> 1)) ^ sv) * 16 + (j4 & 1) * 8;
+}
+
+// Streams one 64-key tile into (kd, vd): wave w copies 16-key group w with
+// direct loads (or zeros for rows past the context / a missing block), and
+// every wave checks all four groups for the abort rule: a row whose context
+// [0, lim] reaches an invalid block is never written (paged_attention_v2.metal:428).
+template <int D>
+__device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* bts, int kvh,
+                                           int key0, int kv_len, int lim, int wave, int lane,
+                                           const Lanes<D>& L, BlockWindow& w, bool& aborted,
+                                           f16* kd, f16* vd) {
+  using C = PCfg<D>;
+  int64_t mine = -1;
+#pragma unroll
+  for (int h = 0; h < kWavesP; ++h) {
+    const int k0 = key0 + 16 * h;
+    if (k0 < kv_len) {
+      const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
+      const int64_t phys = window_block(a, bts, bi, w);
+      if (phys < 0 && k0 <= lim) aborted = true;
+      if (h == wave) mine = phys;
+    }
+  }
+  const int k0 = key0 + 16 * wave;
+  const int nvalid = mine < 0 ? 0 : min(16, kv_len - k0);
+  char* kdst = reinterpret_cast<char*>(kd) + 1024 * (wave * C::NI);
+  char* vdst = reinterpret_cast<char*>(vd) + 1024 * (wave * C::NI);
+  if (nvalid > 0) {
+    const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
+    const int row0 = k0 - bi * a.block_size;
+    const char* kb = reinterpret_cast<const char*>(a.kc + mine * a.k_sb + kvh * a.k_sh +
+                                                   row0 * a.k_st);
+    const char* vb = reinterpret_cast<const char*>(a.vc + mine * a.v_sb + kvh * a.v_sh +
+                                                   row0 * a.v_st);
+#pragma unroll
+    for (int q = 0; q < C::NI; ++q) {
+      if (L.row[q] < nvalid) {
+        __builtin_amdgcn_global_load_lds((gbl_void_t*)(kb + L.koff[q]),
+                                         (lds_void_t*)(kdst + 1024 * q), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((gbl_void_t*)(vb + L.voff[q]),
+                                         (lds_void_t*)(vdst + 1024 * q), 16, 0, 0);
+      } else {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
+        *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
       }
     }
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void stage_store(f16* ks, f16* vs, const Stage<D>& st) {
-  using C = PCfg<D>;
+  } else {
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int i = 0; i < C::MAXC; ++i) {
-    const int f = threadIdx.x + i * kThreadsP;
-    if (f < kKT * C::CH) {
-      const int kr = f / C::CH, ch = f % C::CH;
-      *reinterpret_cast<u32x4*>(ks + kr * C::LD + ch * 8) = st.k[i];
-      *reinterpret_cast<u32x4*>(vs + kr * C::LD + ch * 8) = st.v[i];
+    for (int q = 0; q < C::NI; ++q) {
+      *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
+      *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
     }
   }
 }
 
-// One 32-key tile for this wave's 32 query rows: S^T = K Q^T, online
-// softmax, O^T += V^T P^T.
+// One 64-key tile for this wave's 32 query rows: S^T = K Q^T as two
+// independent 32-key MFMA row blocks, online softmax over both, then
+// O^T += V^T P^T over four 16-key groups.
 template <int D>
-__device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kb, const f16* vb,
-                                          int key0, int lim, int k_rd, int v_rd, int hb,
+__device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, const f16* vt,
+                                          int key0, int lim, int hb, const Lanes<D>& L,
                                           const u32x4 (&qb)[PCfg<D>::NK], float& m_run,
                                           float& l_part, f32x16 (&acc)[PCfg<D>::NDT]) {
   using C = PCfg<D>;
-  // S^T = K Q^T : A lane = K[key l%32][hb*D/2 + 8s .. +7].
-  f32x16 sacc;
+  const char* kbytes = reinterpret_cast<const char*>(kt);
+  const char* vbytes = reinterpret_cast<const char*>(vt);
+  // S^T block j: A lane = K[32j + l%32][hb*D/2 + 8s .. +7].
+  f32x16 sacc[2];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[j][r] = 0.f;
 #pragma unroll
   for (int s2 = 0; s2 < C::NK; ++s2) {
-    const u32x4 kA = *reinterpret_cast<const u32x4*>(kb + k_rd + 8 * s2);
-    sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
-                                                  __builtin_bit_cast(f16x8, qb[s2]), sacc, 0,
-                                                  0, 0);
-  }
-  // Lane holds keys 8(r/4) + 4hb + r%4 for query qj.  The mask is only
-  // evaluated when some row of the wave cannot see the whole tile.
-  const int rel = lim - key0;
-  float mx = -INFINITY;
-  if (__builtin_amdgcn_ballot_w64(rel < kKT - 1) != 0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kl = 8 * (r >> 2) + 4 * hb + (r & 3);
-      if (kl > rel) sacc[r] = -INFINITY;
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 kA =
+          *reinterpret_cast<const u32x4*>(kbytes + L.kaddr[s2] + 32 * j * C::ROWB);
+      sacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
+                                                       __builtin_bit_cast(f16x8, qb[s2]),
+                                                       sacc[j], 0, 0, 0);
     }
   }
+  // Lane holds keys 32j + 8(r/4) + 4hb + r%4 for query qj.  The mask is only
+  // evaluated when some row of the wave cannot see the whole tile.
+  const int rel = lim - key0;
+  if (__builtin_amdgcn_ballot_w64(rel < kKT - 1) != 0) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = 32 * j + 8 * (r >> 2) + 4 * hb + (r & 3);
+        if (kl > rel) sacc[j][r] = -INFINITY;
+      }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sacc[0][r], sacc[1][r]));
   mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;
   // Lazy rescale: keep the reference max unless a score exceeds it by more
   // than 2^8 (p stays <= 256, exact in fp16); the wave-uniform branch is
@@ -219,23 +281,26 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kb, c
     m_run = mx;
   }
   const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
-  f16x8 pb[2];
+  // pb[g]: B operand for 16-key group g (keys 16g + 8(i/4) + 4hb + i%4).
+  f16x8 pb[4];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float p = fast_exp2(fmaf(sacc[r], a.scale_log2, -m_sub));
-    pb[r >> 3][r & 7] = f2h(p);
-    l_part += p;
-  }
-  // O^T += V^T P^T; MFMA c covers keys 16c + 4hb + (i%4) + 8(i/4), i < 8.
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(fmaf(sacc[j][r], a.scale_log2, -m_sub));
+      pb[2 * j + (r >> 3)][r & 7] = f2h(p);
+      l_part += p;
+    }
+  // O^T += V^T P^T; V^T for key group g comes from the transposing LDS read.
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const f16* vp = vb + v_rd + (16 * c) * C::LD + 32 * dt;
+    for (int g = 0; g < 4; ++g) {
+      const f16* vp = reinterpret_cast<const f16*>(vbytes + L.vaddr[dt] + 16 * g * C::ROWB);
       const f16x4 lo = lds_tr4(vp);
-      const f16x4 hi = lds_tr4(vp + 8 * C::LD);
+      const f16x4 hi = lds_tr4(vp + 8 * D);
       const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[c], acc[dt], 0, 0, 0);
+      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[g], acc[dt], 0, 0, 0);
     }
   }
 }
@@ -244,8 +309,13 @@ template <int D>
 __global__ void __launch_bounds__(kThreadsP) __attribute__((amdgpu_waves_per_eu(2, 2)))
 paged_prefill_kernel(PrefillArgs a) {
   using C = PCfg<D>;
-  __shared__ __align__(16) f16 ks[2][C::TILE];
-  __shared__ __align__(16) f16 vs[2][C::TILE];
+  // Four distinct arrays (not one indexed array) so the compiler can tell the
+  // tile being read from the tile being filled and does not wait for the
+  // in-flight direct loads before every LDS read.
+  __shared__ __align__(16) f16 k0s[C::TILE];
+  __shared__ __align__(16) f16 k1s[C::TILE];
+  __shared__ __align__(16) f16 v0s[C::TILE];
+  __shared__ __align__(16) f16 v1s[C::TILE];
   __shared__ int red[2][kWavesP];
 
   // XCD-aware placement: the hardware hands consecutive workgroup ids to the
@@ -261,13 +331,13 @@ paged_prefill_kernel(PrefillArgs a) {
   const int tile_x = logical % gx, tile_y = logical / gx;
   const int kvh = tile_y / a.head_chunks;
   const int hchunk = tile_y % a.head_chunks;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
   const int hw = wave % a.heads_per_wg, sub = wave / a.heads_per_wg;
   const int ghead = hchunk * a.heads_per_wg + hw;             // head index in the group
   const bool math = sub < a.subtiles && ghead < a.G;         // this wave computes
   const int head = kvh * a.G + (ghead < a.G ? ghead : 0);
   const int qj = lane & 31, hb = lane >> 5;
-  const int g16 = lane >> 4, i16 = lane & 15;
 
   // Per-lane query token (lanes l and l+32 share token qj).
   const int tok = tile_x * (kQT * a.subtiles) + (sub < a.subtiles ? sub : 0) * kQT + qj;
@@ -301,9 +371,8 @@ paged_prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  // LDS element offsets of this lane's operand reads (constant over tiles).
-  const int k_rd = qj * C::LD + hb * (D / 2);
-  const int v_rd = (4 * hb + (i16 >> 2)) * C::LD + 16 * (g16 & 1) + 4 * (i16 & 3);
+  Lanes<D> L;
+  lanes_init<D>(a, wave, lane, L);
 
   while (true) {
     // Next sequence among the workgroup's unfinished tokens, and its context.
@@ -325,26 +394,27 @@ paged_prefill_kernel(PrefillArgs a) {
     const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
     const int lim = active ? tpos : -1;  // last key position this row may see
 
-    // Two register stages rotate so K/V loads run two tiles ahead of the
-    // math; LDS holds the tile being computed and the next one.
+    // Double buffer: the next tile's direct loads are issued before this
+    // tile's math; one wait + barrier per tile publishes it.
     BlockWindow win;
     window_load(a, bts, 0, win);
-    Stage<D> sa, sb;
-    stage_load<D>(a, bts, kvh, 0, kv_len, lim, win, aborted, sa);
-    if (n_kt > 1) stage_load<D>(a, bts, kvh, kKT, kv_len, lim, win, aborted, sb);
-    stage_store<D>(ks[0], vs[0], sa);
-    __syncthreads();
+    tile_fetch<D>(a, bts, kvh, 0, kv_len, lim, wave, lane, L, win, aborted, k0s, v0s);
+    wait_all();
+    __builtin_amdgcn_s_barrier();
     for (int kt = 0; kt < n_kt; kt += 2) {
-      if (kt + 2 < n_kt) stage_load<D>(a, bts, kvh, (kt + 2) * kKT, kv_len, lim, win, aborted, sa);
-      if (math) tile_math<D>(a, ks[0], vs[0], kt * kKT, lim, k_rd, v_rd, hb, qb, m_run, l_part, acc);
-      if (kt + 1 < n_kt) stage_store<D>(ks[1], vs[1], sb);
-      __syncthreads();
+      if (kt + 1 < n_kt)
+        tile_fetch<D>(a, bts, kvh, (kt + 1) * kKT, kv_len, lim, wave, lane, L, win, aborted,
+                      k1s, v1s);
+      if (math) tile_math<D>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
+      wait_all();
+      __builtin_amdgcn_s_barrier();
       if (kt + 1 >= n_kt) break;
-      if (kt + 3 < n_kt) stage_load<D>(a, bts, kvh, (kt + 3) * kKT, kv_len, lim, win, aborted, sb);
-      if (math)
-        tile_math<D>(a, ks[1], vs[1], (kt + 1) * kKT, lim, k_rd, v_rd, hb, qb, m_run, l_part, acc);
-      if (kt + 2 < n_kt) stage_store<D>(ks[0], vs[0], sa);
-      __syncthreads();
+      if (kt + 2 < n_kt)
+        tile_fetch<D>(a, bts, kvh, (kt + 2) * kKT, kv_len, lim, wave, lane, L, win, aborted,
+                      k0s, v0s);
+      if (math) tile_math<D>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
+      wait_all();
+      __builtin_amdgcn_s_barrier();
     }
     done = done || active;
   }
@@ -408,6 +478,10 @@ extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
       p->max_blocks_per_seq <= 0 || p->num_blocks <= 0 || p->num_seqs < 0 ||
       num_tokens < 0)
     return fail(VAA_ERR_INVALID_ARG, "vaa_paged_attention_prefill: bad shape params");
+  if (p->block_size % 16 != 0)
+    return fail(VAA_ERR_UNSUPPORTED,
+                "vaa_paged_attention_prefill: block_size=%d is not a multiple of 16",
+                p->block_size);
   if (num_tokens == 0) return VAA_OK;
   if (!query || !key_cache || !value_cache || !block_table || !token_to_seq ||
       !positions || !output)
@@ -437,6 +511,9 @@ extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
   a.num_seqs = p->num_seqs;
   a.max_blocks = p->max_blocks_per_seq;
   a.block_size = p->block_size;
+  a.bs_shift = -1;
+  for (int sh = 4; sh < 31; ++sh)
+    if (p->block_size == (1 << sh)) a.bs_shift = sh;
   a.G = p->queries_per_kv;
   // Waves = (token subtile, head) pairs: 4 heads x 32 tokens when the group
   // has >= 3 heads, 2 x 64 for pairs, 1 x 128 for MHA.
