@@ -172,6 +172,8 @@ def _decode_record(name: str, b, args, partition: int, note: str) -> dict:
     alg = b.decode_algorithmic_bytes()
     used = partition or kernels.choose_partition_size(lens, b.num_kv_heads,
                                                       kernels.device_cus(b.query.device))
+    if used == kernels.PARTITION_BALANCED:
+        used = "balanced"
     return {"workload": name, "note": note, "batch": b.num_seqs,
             "ctx_mean": round(sum(lens) / len(lens), 1), "ctx_max": max(lens),
             "partition": used, "ms_per_step": round(ms, 5),

@@ -50,6 +50,16 @@ enum {
 enum { VAA_INDEX_I32 = 0, VAA_INDEX_I64 = 1 };
 
 /*
+ * vaa_attn_params.partition_size for decode:
+ *   > 0  fixed split-K partitions of that many tokens (a multiple of 128);
+ *   0    automatic, from max_seq_len alone;
+ *   VAA_PARTITION_BALANCED  one workgroup per CU, each taking an equal share
+ *        of the 16-token tiles of all sequences, split on the device from
+ *        seq_lens (for unequal lengths; at most 8192 sequences).
+ */
+#define VAA_PARTITION_BALANCED (-1)
+
+/*
  * Attention parameters.  Mirrors FusedAttentionParams / PagedAttentionParams
  * (vllm_apple/metal/kernels/paged_attention_fused.metal:24-49,
  *  vllm_apple/engine/ops/attention.py:51-157) with 64-bit strides, plus the
@@ -65,7 +75,8 @@ typedef struct vaa_attn_params {
   int32_t num_kv_heads;
   int32_t num_query_heads;
   int32_t queries_per_kv;     /* num_query_heads / num_kv_heads, <= 16        */
-  int32_t partition_size;     /* split-K tokens per partition; 0 = automatic  */
+  int32_t partition_size;     /* split-K tokens per partition; 0 = automatic,
+                                 VAA_PARTITION_BALANCED = split by lengths    */
   int64_t num_blocks;         /* cache capacity in blocks                     */
   int64_t k_stride_block, k_stride_head, k_stride_token;
   int64_t v_stride_block, v_stride_head, v_stride_token;
@@ -161,10 +172,12 @@ size_t vaa_paged_attention_decode_workspace_size(const vaa_attn_params* p,
  * new_values are non-null the token at position L-1 is taken from them and
  * written to the cache in the same launch (the fused KV write); when they are
  * null the cache must already hold it.  Long contexts are split into
- * partitions whose partial (max, sum, acc) go to the workspace and are merged
- * (log-sum-exp) by a second kernel on the same stream; the workspace must hold
- * vaa_paged_attention_decode_workspace_size(p) bytes (it may be null when that
- * size is 0) and must not be shared by calls that can run concurrently.
+ * partitions (p->partition_size, see VAA_PARTITION_BALANCED) whose partial
+ * (max, sum, acc) go to the workspace and are merged (log-sum-exp) by a
+ * second kernel on the same stream; the workspace must hold
+ * vaa_paged_attention_decode_workspace_size(p) bytes, 16-byte aligned (it may
+ * be null when that size is 0), and must not be shared by calls that can run
+ * concurrently.
  */
 int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
                                uint16_t* key_cache, uint16_t* value_cache,

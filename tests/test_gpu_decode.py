@@ -50,7 +50,7 @@ def _run(kc, vc, bt, lens, q, nk, nv, *, layout="kernel", fused=True, part=0, sc
     return out, ref, kd, vd, kc_ref, vc_ref
 
 
-@pytest.mark.parametrize("part", [0, 128, 256, 512])
+@pytest.mark.parametrize("part", [0, 128, 256, 512, -1])
 def test_decode_c1_shape(gpu, part):
     """C1 shape (14q/2kv, D64, GQA 7), fused write, several partition sizes."""
     lens = [37, 512, 16, 201]
@@ -81,8 +81,9 @@ def test_decode_head_shapes(gpu, D, H, KV):
     lens = [1, 15, 16, 17, 300, 1000]
     print(f"[case] shapes D={D} H={H} KV={KV}", flush=True)
     kc, vc, bt, L, q, nk, nv = _case(6, H, KV, D, lens, seed=3)
-    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=128)
-    assert_close(host(out), ref, what=f"decode D={D} H={H} KV={KV}")
+    for part in (128, -1):
+        out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=part)
+        assert_close(host(out), ref, what=f"decode D={D} H={H} KV={KV} part={part}")
 
 
 @pytest.mark.parametrize("bs", [32, 64])
@@ -90,7 +91,7 @@ def test_decode_larger_block_size(gpu, bs):
     """block_size a multiple of 16 (tiles of 16 tokens inside larger blocks)."""
     lens = [1, 31, 33, 2000, 5000, 700]
     kc, vc, bt, L, q, nk, nv = _case(6, 32, 8, 128, lens, bs=bs, seed=13)
-    for part in (0, 128, 1024):
+    for part in (0, 128, 1024, -1):
         out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=part)
         assert_close(host(out), ref, what=f"decode bs={bs} part={part}")
         assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
@@ -100,7 +101,7 @@ def test_decode_long_contexts_many_windows(gpu):
     """Runs longer than one 64-block window per wave (C4-like lengths)."""
     lens = [32768, 20000, 4096, 9999]
     kc, vc, bt, L, q, nk, nv = _case(4, 32, 8, 128, lens, seed=14)
-    for part in (0, 8192, 32768):
+    for part in (0, 8192, 32768, -1):
         out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=part)
         assert_close(host(out), ref, what=f"decode long part={part}")
 
@@ -124,9 +125,10 @@ def test_decode_seq_len_one_is_value_exact(gpu):
 def test_decode_zero_and_edge_lengths(gpu):
     lens = [0, 1, 16, 0, 4097]
     kc, vc, bt, L, q, nk, nv = _case(5, 16, 4, 128, lens, seed=6)
-    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=256)
-    assert_close(host(out), ref, what="decode edge lengths")
-    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[3]) == 0
+    for part in (256, -1):
+        out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=part)
+        assert_close(host(out), ref, what=f"decode edge lengths part={part}")
+        assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[3]) == 0
 
 
 def test_decode_split_matches_unsplit(gpu):
@@ -134,9 +136,12 @@ def test_decode_split_matches_unsplit(gpu):
     kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, lens, seed=7)
     a, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=128)
     b, *_ = _run(kc, vc, bt, L, q, nk, nv, part=8192)
+    c, *_ = _run(kc, vc, bt, L, q, nk, nv, part=-1)
     assert_close(host(a), ref, what="split 128")
     assert_close(host(b), ref, what="split 8192")
+    assert_close(host(c), ref, what="balanced split")
     assert_close(host(a), host(b).astype(np.float64), what="split vs unsplit")
+    assert_close(host(c), host(b).astype(np.float64), what="balanced vs unsplit")
 
 
 def test_decode_outlier_keys_c4_style(gpu):
@@ -147,8 +152,9 @@ def test_decode_outlier_keys_c4_style(gpu):
     flat = kc.view(-1, 128)
     idx = torch.randint(0, flat.shape[0], (flat.shape[0] // 100,), generator=g)
     flat[idx] = (flat[idx].float() * 8).half()
-    out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=512)
-    assert_close(host(out), ref, what="decode outliers")
+    for part in (512, -1):
+        out, ref, *_ = _run(kc, vc, bt, L, q, nk, nv, part=part)
+        assert_close(host(out), ref, what=f"decode outliers part={part}")
 
 
 def test_decode_invalid_block_is_masked(gpu):
@@ -167,3 +173,40 @@ def test_decode_matches_pure_loop_oracle(gpu):
     out, *_ = _run(kc, vc, bt, L, q, nk, nv, fused=False)
     loop = oat.decode_loop_fp32(host(q), host(kc), host(vc), host(bt), host(L), 1 / np.sqrt(32))
     assert_close(host(out), loop, what="vs Metal-structured loop")
+
+
+@pytest.mark.parametrize("seed", [21, 22])
+def test_decode_balanced_ragged_batch(gpu, seed):
+    """Balanced split over many ragged sequences (empty ones included): every
+    piece boundary (inside a sequence, between sequences, across workgroups)
+    against the oracle, with the fused write bit-exact."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, 3000, (77,), generator=g)
+    lens[::9] = 0
+    lens[5] = 1
+    lens = lens.tolist()
+    print(f"[case] balanced ragged seed={seed}", flush=True)
+    kc, vc, bt, L, q, nk, nv = _case(77, 16, 4, 128, lens, seed=seed)
+    out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=-1)
+    assert_close(host(out), ref, what="balanced ragged")
+    assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
+    assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16))
+    zero = [i for i, n in enumerate(lens) if n == 0]
+    assert torch.count_nonzero(out[zero]) == 0
+
+
+def test_decode_balanced_workspace_reuse(gpu):
+    """Two balanced calls in a row through one workspace, the second with fewer
+    and shorter sequences: nothing from the first call leaks into the second."""
+    from vllm_apple_amd import kernels
+
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    for S, hi, seed in ((40, 9000, 31), (7, 700, 32)):
+        g = torch.Generator().manual_seed(seed)
+        lens = torch.randint(1, hi, (S,), generator=g).tolist()
+        kc, vc, bt, L, q, nk, nv = _case(S, 32, 8, 128, lens, seed=seed)
+        out = kernels.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), L.cuda(),
+                                   scale=1 / np.sqrt(128), max_seq_len=max(lens),
+                                   partition_size=-1, workspace=ws)
+        ref = oat.decode(host(q), host(kc), host(vc), host(bt), host(L), 1 / np.sqrt(128))
+        assert_close(host(out), ref, what=f"balanced reuse S={S}")

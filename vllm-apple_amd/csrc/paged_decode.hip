@@ -54,11 +54,18 @@ struct DecodeArgs {
   f16* out;
   const f16* new_k;
   const f16* new_v;
-  float* ws_acc;  // [seq][qhead][part][D] unnormalised partial outputs
-  float* ws_ml;   // [seq][qhead][part][2] (max in log2 domain, sum)
+  // Split-K partials, one row per (piece, query head): unnormalised acc [D]
+  // and (max in the log2 domain, sum).  Fixed partitions use rows
+  // (seq*H + qhead)*max_parts + part; the balanced split uses
+  // (kvh*(max_parts + num_seqs) + c + seq)*G + h, with max_parts = workgroups
+  // per kv head, and keeps its geometry in ws_hdr (per, starts[0..num_seqs]).
+  float* ws_acc;
+  float* ws_ml;
+  int* ws_hdr;
   float scale_log2;
   int num_seqs, max_blocks, block_size, num_kv_heads, num_q_heads, G;
   int part_tiles, max_parts;
+  int lds_main;  // bytes of LDS before the balanced split's prefix sums
   int64_t num_blocks;
   int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
   int64_t q_st, q_sh, o_st, o_sh, n_st, n_sh;
@@ -181,42 +188,33 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
   }
 }
 
+// Where the result of one (sequence, kv head, tile range) goes.
+struct RangeOut {
+  bool whole;         // the range is the whole sequence: normalised fp16 rows of out
+  int64_t prow0;      // else: workspace row of the group's first query head
+  int64_t prow_step;  // workspace row stride between the group's query heads
+};
+
+// The 8 waves of the workgroup attend query heads kvh*G .. kvh*G+G-1 of
+// sequence seq over the 16-token tiles [t0, t1) of its first L (clamped)
+// positions: each wave streams a contiguous run of tiles, then the waves
+// combine through LDS.  smem is reused on return only after the trailing
+// barrier, so a workgroup may call this repeatedly.
 template <int D>
-__global__ void __launch_bounds__(kWaves* kWave)
-paged_decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
+                                             int kvh, int L, bool fused, int t0, int t1,
+                                             const RangeOut& ro, bool trailing_barrier) {
   using C = Cfg<D>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int c16 = lane & 15, g = lane >> 4;
   const int G = a.G;
-
-  int L = a.seq_lens[seq];
-  const int Lorig = L;
-  const int cap = a.max_blocks * a.block_size;
-  if (L > cap) L = cap;
-  if (L <= 0) {
-    if (part == 0) {
-      for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-        const int h = kvh * G + idx / D;
-        a.out[seq * a.o_st + h * a.o_sh + idx % D] = f2h(0.f);
-      }
-    }
-    return;
-  }
-  const int part_tok = a.part_tiles * kTile;
   const int n_tiles = (L + kTile - 1) / kTile;
-  const int n_parts = min((L + part_tok - 1) / part_tok, a.max_parts);
-  if (part >= n_parts) return;
-  const int t0 = part * a.part_tiles;
-  const int t1 = (part == a.max_parts - 1) ? n_tiles : min(t0 + a.part_tiles, n_tiles);
   const int per = (t1 - t0 + kWaves - 1) / kWaves;
   const int jb = t0 + wave * per;
   const int je = min(jb + per, t1);
 
   // The sequence's last tile is peeled when it is partial or holds the new
   // token (fused KV write); every other tile is full and runs the pipeline.
-  const bool fused = a.new_k != nullptr && Lorig == L;
   const int special = (fused || (L % kTile) != 0) ? n_tiles - 1 : n_tiles;
   const int jm = min(je, special);
 
@@ -353,8 +351,6 @@ paged_decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
-  const int H = a.num_q_heads;
-  const bool single = (n_parts == 1);
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
@@ -371,11 +367,11 @@ paged_decode_kernel(DecodeArgs a) {
         den += sc * wl[w * 16 + h];
       }
     }
-    const int qh = kvh * G + h;
-    if (single) {
+    if (ro.whole) {
+      const int qh = kvh * G + h;
       a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
     } else {
-      const int64_t row = (static_cast<int64_t>(seq) * H + qh) * a.max_parts + part;
+      const int64_t row = ro.prow0 + h * ro.prow_step;
       a.ws_acc[row * D + d] = num;
       if (d == 0) {
         a.ws_ml[row * 2 + 0] = M;
@@ -383,6 +379,169 @@ paged_decode_kernel(DecodeArgs a) {
       }
     }
   }
+  if (trailing_barrier) __syncthreads();
+}
+
+// Zero output rows of a sequence with seq_len <= 0 (the reference leaves them
+// unwritten in a pre-zeroed buffer).
+__device__ __forceinline__ void zero_rows(const DecodeArgs& a, int seq, int h0, int nh, int D) {
+  for (int idx = threadIdx.x; idx < nh * D; idx += blockDim.x) {
+    const int h = h0 + idx / D;
+    a.out[seq * a.o_st + h * a.o_sh + idx % D] = f2h(0.f);
+  }
+}
+
+__device__ __forceinline__ int clamped_len(const DecodeArgs& a, int seq) {
+  const int L = a.seq_lens[seq];
+  const int cap = a.max_blocks * a.block_size;
+  return L > cap ? cap : L;
+}
+
+// Fixed partitions: grid (partition, kv_head, seq).
+template <int D>
+__global__ void __launch_bounds__(kWaves* kWave)
+paged_decode_kernel(DecodeArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int G = a.G;
+  const int Lorig = a.seq_lens[seq];
+  const int L = clamped_len(a, seq);
+  if (L <= 0) {
+    if (part == 0) zero_rows(a, seq, kvh * G, G, D);
+    return;
+  }
+  const int part_tok = a.part_tiles * kTile;
+  const int n_tiles = (L + kTile - 1) / kTile;
+  const int n_parts = min((L + part_tok - 1) / part_tok, a.max_parts);
+  if (part >= n_parts) return;
+  const int t0 = part * a.part_tiles;
+  const int t1 = (part == a.max_parts - 1) ? n_tiles : min(t0 + a.part_tiles, n_tiles);
+  RangeOut ro;
+  ro.whole = (n_parts == 1);
+  ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + kvh * G) * a.max_parts + part;
+  ro.prow_step = a.max_parts;
+  decode_range<D>(a, smem, seq, kvh, L, a.new_k != nullptr && Lorig == L, t0, t1, ro, false);
+}
+
+// Balanced split: the tiles of all sequences (for one kv head) are laid end
+// to end and workgroup c of the kv head takes tiles [c*per, (c+1)*per), with
+// per = max(ceil(total / gridDim.x), kBalMinTiles).  Every workgroup derives
+// the same prefix sums of tiles per sequence from seq_lens, so the split
+// follows the actual lengths without a host round trip.  A sequence inside
+// one workgroup's range is finished there; the pieces of a sequence that
+// crosses ranges go to workspace rows (kvh*(gridDim.x + num_seqs) + c + seq)*G
+// + h -- distinct for distinct (c, seq) because the ranges and the sequences
+// are both in increasing order -- and the merge kernel combines them.
+constexpr int kBalMinTiles = 4 * kWaves;
+
+__device__ __forceinline__ int tiles_of(const DecodeArgs& a, int seq) {
+  const int L = clamped_len(a, seq);
+  return L > 0 ? (L + kTile - 1) / kTile : 0;
+}
+
+// starts[s] = sum of tiles_of(s') for s' < s, s = 0..num_seqs (LDS).
+__device__ __forceinline__ void tile_prefix(const DecodeArgs& a, int* starts, int* wsum) {
+  const int B = a.num_seqs, nt = blockDim.x;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int per = (B + nt - 1) / nt;
+  const int s0 = min(B, static_cast<int>(threadIdx.x) * per), s1 = min(B, s0 + per);
+  int sum = 0;
+  for (int s = s0; s < s1; ++s) sum += tiles_of(a, s);
+  int x = sum;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == kWave - 1) wsum[wave] = x;
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; ++w) off += wsum[w];
+  int run = off + x - sum;
+  for (int s = s0; s < s1; ++s) {
+    starts[s] = run;
+    run += tiles_of(a, s);
+  }
+  if (threadIdx.x == nt - 1) starts[B] = off + x;
+  __syncthreads();
+}
+
+template <int D>
+__global__ void __launch_bounds__(kWaves* kWave)
+paged_decode_balanced_kernel(DecodeArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int c = blockIdx.x, kvh = blockIdx.y, nc = gridDim.x;
+  const int B = a.num_seqs, G = a.G;
+  int* starts = reinterpret_cast<int*>(smem + a.lds_main);
+  tile_prefix(a, starts, starts + B + 1);
+  const int total = starts[B];
+  const int per = max((total + nc - 1) / nc, kBalMinTiles);
+  if (c == 0 && kvh == 0) {
+    // Split geometry for the merge kernel.
+    if (threadIdx.x == 0) a.ws_hdr[0] = per;
+    for (int s = threadIdx.x; s <= B; s += blockDim.x) a.ws_hdr[1 + s] = starts[s];
+  }
+  const int r0 = c * per, r1 = min(total, r0 + per);
+  if (r0 >= r1) return;
+  // First sequence with tiles at or after r0.
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (starts[mid + 1] <= r0) lo = mid + 1;
+    else hi = mid;
+  }
+  int seq = lo;
+  for (int pos = r0; pos < r1; ++seq) {
+    const int s0 = starts[seq], s1 = starts[seq + 1];
+    if (s1 <= pos) continue;  // empty sequence
+    const int t0 = pos - s0, t1 = min(r1, s1) - s0;
+    RangeOut ro;
+    ro.whole = (t0 == 0 && t1 == s1 - s0);
+    ro.prow0 = (static_cast<int64_t>(kvh) * (nc + B) + c + seq) * G;
+    ro.prow_step = 1;
+    const int L = clamped_len(a, seq);
+    decode_range<D>(a, smem, seq, kvh, L, a.new_k != nullptr && a.seq_lens[seq] == L, t0, t1,
+                    ro, true);
+    pos = s0 + t1;
+  }
+}
+
+// Merge for the balanced split: sequence seq spans workgroups
+// starts[seq]/per .. (starts[seq+1]-1)/per of its kv head; when that is one
+// workgroup the decode kernel wrote the row already.  Rows of empty
+// sequences are zeroed here.
+template <int D>
+__global__ void __launch_bounds__(D)
+paged_decode_merge_balanced_kernel(DecodeArgs a) {
+  const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+  const int G = a.G, B = a.num_seqs, nc = a.max_parts;
+  const int L = clamped_len(a, seq);
+  if (L <= 0) {
+    a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(0.f);
+    return;
+  }
+  const int per = a.ws_hdr[0];
+  const int c0 = a.ws_hdr[1 + seq] / per, c1 = (a.ws_hdr[2 + seq] - 1) / per;
+  if (c0 == c1) return;
+  const int kvh = qh / G, h = qh % G;
+  const int64_t base = static_cast<int64_t>(kvh) * (nc + B) + seq;
+  float M = -INFINITY;
+  for (int c = c0; c <= c1; ++c) {
+    const int64_t row = (base + c) * G + h;
+    if (a.ws_ml[row * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[row * 2]);
+  }
+  float num = 0.f, den = 0.f;
+  if (M != -INFINITY) {
+    for (int c = c0; c <= c1; ++c) {
+      const int64_t row = (base + c) * G + h;
+      const float lp = a.ws_ml[row * 2 + 1];
+      if (!(lp > 0.f)) continue;
+      const float sc = fast_exp2(a.ws_ml[row * 2] - M);
+      num += sc * a.ws_acc[row * D + d];
+      den += sc * lp;
+    }
+  }
+  a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
 }
 
 // Second pass for split sequences:
@@ -429,32 +588,68 @@ int num_cus() {
   return n;
 }
 
-// Automatic partition size from max_seq_len alone (all sequences assumed at
-// the maximum): split only as far as needed for the workgroups to cover every
-// CU once, in multiples of 16 * kWaves tokens.  Callers that know the lengths
-// pass partition_size explicitly.
-int choose_partition(const vaa_attn_params* p, int* part_out, int* max_parts_out) {
+constexpr int kBalMaxSeqs = 8192;  // prefix sums of tiles per sequence live in LDS
+
+// How a call splits its sequences.
+struct Split {
+  bool balanced;     // balanced split over the actual lengths
+  int part;          // fixed: tokens per partition (balanced: -1)
+  int max_parts;     // fixed: partitions per sequence; balanced: workgroups per kv head
+  size_t ws_bytes;   // workspace needed (0: none)
+  size_t hdr_bytes;  // balanced: bytes before the partial rows
+};
+
+// Fixed partitions with partition_size > 0; with 0 the size comes from
+// max_seq_len alone (all sequences assumed at the maximum): split only as far
+// as needed for the workgroups to cover every CU once, in multiples of
+// 16 * kWaves tokens.  VAA_PARTITION_BALANCED: one workgroup per CU, each
+// taking an equal share of the tiles of all sequences (split on the device
+// from seq_lens).
+int plan_split(const vaa_attn_params* p, Split* sp) {
   const int64_t cap = static_cast<int64_t>(p->max_blocks_per_seq) * p->block_size;
   int64_t max_len = p->max_seq_len;
   if (max_len > cap) max_len = cap;
   if (max_len < 1) max_len = 1;
   const int quantum = kTile * kWaves;
   int64_t part = p->partition_size;
+  const size_t row_bytes = (static_cast<size_t>(p->head_size) + 2) * sizeof(float);
+  if (part == VAA_PARTITION_BALANCED) {
+    if (p->num_seqs > kBalMaxSeqs)
+      return fail(VAA_ERR_UNSUPPORTED, "balanced split: num_seqs=%d > %d", p->num_seqs,
+                  kBalMaxSeqs);
+    const int wgs = (num_cus() + p->num_kv_heads - 1) / p->num_kv_heads;
+    sp->balanced = true;
+    sp->part = VAA_PARTITION_BALANCED;
+    sp->max_parts = wgs < 1 ? 1 : wgs;
+    sp->hdr_bytes = ((static_cast<size_t>(p->num_seqs) + 2) * sizeof(int) + 255) / 256 * 256;
+    const size_t rows = static_cast<size_t>(p->num_kv_heads) * (sp->max_parts + p->num_seqs) *
+                        p->queries_per_kv;
+    sp->ws_bytes = sp->hdr_bytes + rows * row_bytes;
+    return VAA_OK;
+  }
   if (part > 0) {
     if (part % quantum != 0)
       return fail(VAA_ERR_INVALID_ARG,
                   "partition_size=%lld must be a positive multiple of %d",
                   (long long)part, quantum);
-  } else {
+  } else if (part == 0) {
     const int64_t pairs = static_cast<int64_t>(p->num_seqs) * p->num_kv_heads;
     int64_t splits = pairs > 0 ? (num_cus() + pairs - 1) / pairs : 1;
     if (splits < 1) splits = 1;
     part = (max_len + splits - 1) / splits;
     part = (part + quantum - 1) / quantum * quantum;
+  } else {
+    return fail(VAA_ERR_INVALID_ARG, "partition_size=%lld (use > 0, 0 or %d)",
+                (long long)part, VAA_PARTITION_BALANCED);
   }
   if (part > (int64_t{1} << 30)) part = int64_t{1} << 30;
-  *part_out = static_cast<int>(part);
-  *max_parts_out = static_cast<int>((max_len + part - 1) / part);
+  sp->balanced = false;
+  sp->part = static_cast<int>(part);
+  sp->max_parts = static_cast<int>((max_len + part - 1) / part);
+  sp->hdr_bytes = 0;
+  sp->ws_bytes = sp->max_parts <= 1 ? 0
+                                    : static_cast<size_t>(p->num_seqs) * p->num_query_heads *
+                                          sp->max_parts * row_bytes;
   return VAA_OK;
 }
 
@@ -495,16 +690,28 @@ int check_params(const vaa_attn_params* p, const char* what) {
 }
 
 template <int D>
-int launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t stream) {
+int launch_decode(const DecodeArgs& a0, bool balanced, hipStream_t stream) {
+  DecodeArgs a = a0;
   const size_t lds_tiles = static_cast<size_t>(kWaves) * kTile * D * sizeof(f16);
   const size_t lds_comb =
       (2 * kWaves * 16 + static_cast<size_t>(kWaves) * a.G * D) * sizeof(float);
   const size_t lds = lds_tiles > lds_comb ? lds_tiles : lds_comb;
-  dim3 grid(a.max_parts, a.num_kv_heads, num_seqs);
+  if (balanced) {
+    a.lds_main = static_cast<int>((lds + 15) / 16 * 16);
+    const size_t lds_b = a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kWaves) * sizeof(int);
+    hipLaunchKernelGGL(paged_decode_balanced_kernel<D>, dim3(a.max_parts, a.num_kv_heads),
+                       dim3(kWaves * kWave), lds_b, stream, a);
+    int st = check_launch("paged_decode_balanced_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(paged_decode_merge_balanced_kernel<D>, dim3(a.num_q_heads, a.num_seqs),
+                       dim3(D), 0, stream, a);
+    return check_launch("paged_decode_merge_balanced_kernel");
+  }
+  dim3 grid(a.max_parts, a.num_kv_heads, a.num_seqs);
   hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kWaves * kWave), lds, stream, a);
   int st = check_launch("paged_decode_kernel");
   if (st || a.max_parts <= 1) return st;
-  hipLaunchKernelGGL(paged_decode_merge_kernel<D>, dim3(a.num_q_heads, num_seqs), dim3(D),
+  hipLaunchKernelGGL(paged_decode_merge_kernel<D>, dim3(a.num_q_heads, a.num_seqs), dim3(D),
                      0, stream, a);
   return check_launch("paged_decode_merge_kernel");
 }
@@ -516,14 +723,13 @@ using namespace vaa;
 
 extern "C" size_t vaa_paged_attention_decode_workspace_size(const vaa_attn_params* p,
                                                             int32_t* partition_size_out) {
-  if (!p || p->num_seqs <= 0 || p->block_size <= 0 || p->max_blocks_per_seq <= 0)
+  if (!p || p->num_seqs <= 0 || p->block_size <= 0 || p->max_blocks_per_seq <= 0 ||
+      p->num_kv_heads <= 0 || p->queries_per_kv <= 0)
     return 0;
-  int part, max_parts;
-  if (choose_partition(p, &part, &max_parts) != VAA_OK) return 0;
-  if (partition_size_out) *partition_size_out = part;
-  if (max_parts <= 1) return 0;
-  return static_cast<size_t>(p->num_seqs) * p->num_query_heads * max_parts *
-         (p->head_size + 2) * sizeof(float);
+  Split sp;
+  if (plan_split(p, &sp) != VAA_OK) return 0;
+  if (partition_size_out) *partition_size_out = sp.part;
+  return sp.ws_bytes;
 }
 
 extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
@@ -552,8 +758,8 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache))
     return fail(VAA_ERR_INVALID_ARG,
                 "vaa_paged_attention_decode: query and caches must be 16-byte aligned");
-  int part, max_parts;
-  st = choose_partition(p, &part, &max_parts);
+  Split sp;
+  st = plan_split(p, &sp);
   if (st) return st;
 
   DecodeArgs a;
@@ -567,14 +773,19 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   a.new_v = reinterpret_cast<const f16*>(new_values);
   a.ws_acc = nullptr;
   a.ws_ml = nullptr;
-  if (max_parts > 1) {
-    const size_t need = vaa_paged_attention_decode_workspace_size(p, nullptr);
-    if (!workspace || workspace_bytes < need)
+  a.ws_hdr = nullptr;
+  if (sp.ws_bytes > 0) {
+    if (!workspace || workspace_bytes < sp.ws_bytes)
       return fail(VAA_ERR_WORKSPACE,
                   "vaa_paged_attention_decode: workspace %zu bytes < %zu needed",
-                  workspace_bytes, need);
-    const size_t rows = static_cast<size_t>(p->num_seqs) * p->num_query_heads * max_parts;
-    a.ws_acc = static_cast<float*>(workspace);
+                  workspace_bytes, sp.ws_bytes);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+      return fail(VAA_ERR_INVALID_ARG,
+                  "vaa_paged_attention_decode: workspace must be 16-byte aligned");
+    const size_t rows = (sp.ws_bytes - sp.hdr_bytes) / ((p->head_size + 2) * sizeof(float));
+    unsigned char* base = static_cast<unsigned char*>(workspace);
+    a.ws_hdr = reinterpret_cast<int*>(base);
+    a.ws_acc = reinterpret_cast<float*>(base + sp.hdr_bytes);
     a.ws_ml = a.ws_acc + rows * p->head_size;
   }
   a.scale_log2 = p->scale * kLog2e;
@@ -584,8 +795,9 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   a.num_kv_heads = p->num_kv_heads;
   a.num_q_heads = p->num_query_heads;
   a.G = p->queries_per_kv;
-  a.part_tiles = part / kTile;
-  a.max_parts = max_parts;
+  a.part_tiles = sp.balanced ? 0 : sp.part / kTile;
+  a.max_parts = sp.max_parts;
+  a.lds_main = 0;
   a.num_blocks = p->num_blocks;
   a.k_sb = p->k_stride_block; a.k_sh = p->k_stride_head; a.k_st = p->k_stride_token;
   a.v_sb = p->v_stride_block; a.v_sh = p->v_stride_head; a.v_st = p->v_stride_token;
@@ -595,10 +807,10 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (p->head_size) {
-    case 32: return launch_decode<32>(a, p->num_seqs, s);
-    case 64: return launch_decode<64>(a, p->num_seqs, s);
-    case 96: return launch_decode<96>(a, p->num_seqs, s);
-    case 128: return launch_decode<128>(a, p->num_seqs, s);
+    case 32: return launch_decode<32>(a, sp.balanced, s);
+    case 64: return launch_decode<64>(a, sp.balanced, s);
+    case 96: return launch_decode<96>(a, sp.balanced, s);
+    case 128: return launch_decode<128>(a, sp.balanced, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
 }

@@ -28,6 +28,9 @@ VAA_ERR_WORKSPACE = -4
 VAA_INDEX_I32 = 0
 VAA_INDEX_I64 = 1
 
+# partition_size value asking decode to split by the actual lengths on the device.
+VAA_PARTITION_BALANCED = -1
+
 
 class NativeLibraryError(RuntimeError):
     """The HIP library could not be loaded (not built, or wrong platform)."""

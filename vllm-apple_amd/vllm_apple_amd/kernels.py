@@ -220,8 +220,13 @@ def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
 
 
 # Decode launch geometry (paged_decode.hip): one workgroup of 8 waves per CU
-# at a time, partitions in multiples of 128 tokens.
+# at a time, partitions in multiples of 128 tokens; the balanced split gives
+# each workgroup at least 32 tiles (512 tokens) and takes at most 8192
+# sequences.
 _DECODE_QUANTUM = 128
+_BALANCED_MIN_TOKENS = 512
+_BALANCED_MAX_SEQS = 8192
+PARTITION_BALANCED = _lib.VAA_PARTITION_BALANCED
 _num_cus: dict[int, int] = {}
 
 
@@ -234,14 +239,18 @@ def device_cus(device: torch.device | None = None) -> int:
 
 def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
                           merge_tokens: int = 256, wg_tokens: int = 96) -> int:
-    """Split-K partition (tokens) for known sequence lengths.
+    """Split-K mode for known sequence lengths: a partition size in tokens, or
+    PARTITION_BALANCED.
 
-    Estimates the step time in "tokens of one kv head streamed by one CU" for
-    each candidate P: the list-scheduling makespan max(total/m, largest piece)
-    plus half a piece of tail when there is more than one wave of workgroups,
-    a fixed workgroup start-up cost and, when any sequence is split, the merge
-    launch.  Equal lengths that already cover the CUs are left unsplit.
-    Memoised per length tuple (the same step is decoded by every layer).
+    Estimates the step time in "tokens of one kv head streamed by one CU".
+    Fixed partitions of P tokens: the list-scheduling makespan
+    max(total/m, largest piece) plus half a piece of tail when there is more
+    than one wave of workgroups, a start-up cost per workgroup and, when any
+    sequence is split, the merge launch.  Balanced split: total/m plus one
+    start-up per sequence piece a workgroup meets and the merge launch, which
+    it always has.  Equal lengths that already cover the CUs stay unsplit;
+    the balanced split must win by 3 % to be chosen.  Memoised per length
+    tuple (the same step is decoded by every layer).
     """
     key = (tuple(int(x) for x in seq_lens_host), int(num_kv_heads), int(num_cus),
            merge_tokens, wg_tokens)
@@ -265,7 +274,14 @@ def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
     big = np.minimum(P, longest).astype(np.float64)
     t = np.maximum(total / m, big) + np.where(wgs > m, big / 2, 0.0) + wg_tokens * wgs / m
     t = t + np.where(longest > P, merge_tokens, 0)
-    best = int(P[int(np.argmin(t))])
+    i = int(np.argmin(t))
+    best, t_fix = int(P[i]), float(t[i])
+    if lens.size <= _BALANCED_MAX_SEQS:
+        c = (m + num_kv_heads - 1) // num_kv_heads
+        per = max(total / (c * num_kv_heads), float(_BALANCED_MIN_TOKENS))
+        t_bal = per + wg_tokens * (1.0 + lens.size / c) + merge_tokens
+        if t_bal < 0.97 * t_fix:
+            best = PARTITION_BALANCED
     if len(_partition_cache) > 4096:
         _partition_cache.clear()
     _partition_cache[key] = best
@@ -288,7 +304,8 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
     seq_lens[s]-1 is written to the cache by the same launch (fused KV write).
     max_seq_len must bound seq_lens (it sizes the split-K grid).  With
     seq_lens_host (host copies of the lengths, no device sync needed) and
-    partition_size 0 the split-K partition is chosen from the actual lengths.
+    partition_size 0 the split-K mode is chosen from the actual lengths;
+    partition_size PARTITION_BALANCED splits by the lengths on the device.
     """
     _require_gpu(query, key_cache, value_cache, block_table, seq_lens, output, new_keys, new_values)
     _require_dtype(query, torch.float16, "query")
