@@ -33,6 +33,15 @@ SOURCES = [
 
 ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")
 
+# Per-source flags.  The prefill kernel's row maxima take fmaxf over MFMA
+# results; under IEEE NaN rules each operand is first canonicalised (one extra
+# v_max_f32 per score).  Scores are finite or the -inf of a masked key, so
+# the kernel is built without NaN semantics (infinities are kept): 3.5 %
+# faster on C3.
+FILE_FLAGS = {
+    "paged_prefill.hip": ["-fno-honor-nans"],
+}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -58,7 +67,8 @@ def common_flags() -> list[str]:
 
 def _compile(src: str) -> Path:
     obj = OBJ_DIR / (Path(src).stem + ".o")
-    cmd = [hipcc(), *common_flags(), "-c", str(HERE / src), "-o", str(obj)]
+    cmd = [hipcc(), *common_flags(), *FILE_FLAGS.get(src, []), "-c", str(HERE / src), "-o",
+           str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
