@@ -8,7 +8,8 @@
  * thread-local message for the last failure on the calling thread.
  *
  * Data types: K/V cache, queries, outputs and activations are IEEE fp16
- * (uint16_t storage).  Block tables, sequence lengths, token->sequence maps
+ * (uint16_t storage); the attention entry points also take bfloat16 through
+ * vaa_attn_params.dtype.  Block tables, sequence lengths, token->sequence maps
  * and positions are int32.  Slot mappings may be int32 (engine) or int64
  * (vLLM metadata), selected by an argument.
  *
@@ -36,7 +37,7 @@
 extern "C" {
 #endif
 
-#define VAA_ABI_VERSION 1
+#define VAA_ABI_VERSION 2
 
 enum {
   VAA_OK = 0,
@@ -48,6 +49,9 @@ enum {
 
 /* Index element types for slot mappings. */
 enum { VAA_INDEX_I32 = 0, VAA_INDEX_I64 = 1 };
+
+/* 16-bit element types of caches, queries, new K/V and outputs. */
+enum { VAA_DTYPE_F16 = 0, VAA_DTYPE_BF16 = 1 };
 
 /*
  * vaa_attn_params.partition_size for decode:
@@ -83,6 +87,9 @@ typedef struct vaa_attn_params {
   int64_t q_stride_token, q_stride_head;
   int64_t o_stride_token, o_stride_head;
   int64_t new_kv_stride_token, new_kv_stride_head; /* new K and new V        */
+  int32_t dtype;              /* VAA_DTYPE_F16 (0, the reference's type) or
+                                 VAA_DTYPE_BF16: element type of the cache,
+                                 queries, new K/V and outputs; fp32 math      */
 } vaa_attn_params;
 
 /* Thread-local message describing the last error on this thread. */

@@ -50,16 +50,34 @@ def test_python_binding_covers_the_header(lib):
     assert set(_lib.SIGNATURES) == set(declared_functions())
 
 
-def test_params_struct_layout_matches_header():
-    """ctypes mirror of vaa_attn_params: 10 int32/float fields then 13 int64."""
+def test_params_struct_layout_matches_header(tmp_path):
+    """The ctypes mirror of vaa_attn_params has the header's size and field
+    offsets, as gcc lays the struct out from include/vllm_apple_amd.h."""
+    import shutil
+    import subprocess
+
     from vllm_apple_amd import _lib
 
-    assert ctypes.sizeof(_lib.VaaAttnParams) == 10 * 4 + 13 * 8
-    assert _lib.VaaAttnParams.num_blocks.offset == 40
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    names = [f[0] for f in _lib.VaaAttnParams._fields_]
+    prog = tmp_path / "layout.c"
+    prog.write_text(
+        "#include <stdio.h>\n#include <stddef.h>\n#include \"vllm_apple_amd.h\"\n"
+        "int main(void) {\n  printf(\"%zu\\n\", sizeof(vaa_attn_params));\n"
+        + "".join(f'  printf("%zu\\n", offsetof(vaa_attn_params, {n}));\n' for n in names)
+        + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{REPO / 'include'}", str(prog), "-o", str(exe)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(_lib.VaaAttnParams)
+    assert got[1:] == [getattr(_lib.VaaAttnParams, n).offset for n in names]
 
 
 def test_version_and_error_string_without_gpu(lib):
-    assert lib.vaa_abi_version() == 1
+    assert lib.vaa_abi_version() == 2
     from vllm_apple_amd import _lib
 
     assert isinstance(_lib.last_error(), str)

@@ -96,12 +96,13 @@ def test_forward_mixed_batch_vllm_cache(gpu):
     assert_close(host(out), ref, what="forward mixed")
 
 
-def test_forward_bf16_activations(gpu):
-    """bf16 model: activations run in fp16, output copied back to bf16; the
-    bf16 kv_cache is replaced by an fp16 cache of the same shape."""
+def test_forward_bf16_native_cache(gpu):
+    """bf16 model: the bf16 vLLM kv_cache is written in place (bit-exact 16-bit
+    copies) and attention runs in bf16, with no fp16 copy of the cache and no
+    conversions (the reference converts to fp16, metal_attn.py:609-620)."""
     from vllm_apple_amd.backend import HipAttentionImpl
 
-    b = _mixed_batch(seed=2, dtype=torch.bfloat16, dec_lens=(40, 7), pre=((64, 20),))
+    b = _mixed_batch(seed=2, dtype=torch.bfloat16, dec_lens=(40, 7, 1000), pre=((64, 20),))
     H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
     scale = 1 / math.sqrt(D)
     impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
@@ -112,14 +113,57 @@ def test_forward_bf16_activations(gpu):
     v = qkv[:, (H + KV) * D:].view(T, KV, D)
     kv_cache = b["kv_cache"].to(dev)
     out = torch.zeros((T, H, D), dtype=torch.bfloat16, device=dev)
-    # The fp16 cache starts as a copy of the bf16 cache's contents for this test.
-    impl._shadow = kv_cache.to(torch.float16)
     impl.forward(None, q, k, v, kv_cache, _metadata(b, dev), output=out)
     torch.cuda.synchronize()
-    ref, _, _ = _oracle(b, scale)
+    assert impl._shadow is None, "no fp16 copy of a bf16 cache"
+    # Oracle: the KV write on the bf16 bit patterns, attention on their values.
+    bits = lambda t: t.cpu().view(torch.float16).numpy()  # noqa: E731
+    qkv_b = bits(b["qkv"])
+    kc, vc = bits(b["kv_cache"][0]).copy(), bits(b["kv_cache"][1]).copy()
+    okv.kv_write_slots(kc, vc, qkv_b[:, H * D:(H + KV) * D].reshape(T, KV, D),
+                       qkv_b[:, (H + KV) * D:].reshape(T, KV, D), b["slots"].numpy(), "vllm")
+    assert np.array_equal(bits(kv_cache[0]).view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(bits(kv_cache[1]).view(np.uint16), vc.view(np.uint16))
+    val = lambda a: torch.from_numpy(a.copy()).view(torch.bfloat16).float().numpy()  # noqa: E731
+    qv = b["qkv"].float().numpy()[:, :H * D].reshape(T, H, D)
+    kcv, vcv = val(kc), val(vc)
+    nd = b["num_decode"]
+    ref = np.zeros((T, H, D))
+    ref[:nd] = oat.decode(qv[:nd], kcv, vcv, b["bt"].numpy()[:nd], b["lens"].numpy()[:nd],
+                          scale, "vllm")
+    pre, _ = oat.prefill(qv, kcv, vcv, b["bt"].numpy(), b["tok"], b["pos"], scale, "vllm",
+                         rows=np.arange(nd, T))
+    ref[nd:] = pre[nd:]
+    assert out.dtype == torch.bfloat16
+    # bf16 bound (tests/test_gpu_bf16.py): 8x the fp16 absolute bound.
+    assert_close(out.float().cpu().numpy(), ref, atol=1.6e-2, rtol=1e-2, what="bf16 forward")
+
+
+def test_forward_bf16_activations_fp16_cache(gpu):
+    """bf16 activations over an fp16 cache: converted to the cache's type and
+    the output converted back, as the reference does for its fp16 kernels."""
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    b = _mixed_batch(seed=6, dtype=torch.float16, dec_lens=(40, 7), pre=((64, 20),))
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    scale = 1 / math.sqrt(D)
+    impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv16 = b["qkv"].to(dev)
+    qkv = qkv16.to(torch.bfloat16)
+    b["qkv"] = qkv.to(torch.float16).cpu()   # the oracle sees the bf16-rounded inputs
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    kv_cache = b["kv_cache"].to(dev)
+    out = torch.zeros((T, H, D), dtype=torch.bfloat16, device=dev)
+    impl.forward(None, q, k, v, kv_cache, _metadata(b, dev), output=out)
+    torch.cuda.synchronize()
+    ref, kc, vc = _oracle(b, scale)
+    assert np.array_equal(host(kv_cache[0]).view(np.uint16), kc.view(np.uint16))
     assert out.dtype == torch.bfloat16
     # bf16 output rounding (8-bit mantissa) on top of the fp16 path.
-    assert_close(host(out.float()), ref, atol=2e-3, rtol=1e-2 + 2 ** -8, what="bf16 forward")
+    assert_close(host(out.float()), ref, atol=2e-3, rtol=1e-2 + 2 ** -8, what="bf16 over fp16")
 
 
 def test_forward_encoder_only_bidirectional(gpu):

@@ -18,6 +18,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+typedef __bf16 bf16;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4v __attribute__((ext_vector_type(4)));
+
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -51,6 +56,56 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
+
+// ------------------------------------------------- 16-bit element types --
+// The attention kernels keep K/V/Q/outputs as raw 16-bit storage and are
+// templated on the element type only where values are converted or fed to
+// the matrix cores: IEEE fp16 (f16) or bfloat16 (bf16), both with fp32
+// accumulation.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<f16> {
+  using x4 = f16x4;
+  using x8 = f16x8;
+  static __device__ __forceinline__ float to_f(f16 v) { return static_cast<float>(v); }
+  static __device__ __forceinline__ f16 from_f(float v) { return static_cast<f16>(v); }
+  // D[16x16] += A[16x32] B[32x16]
+  static __device__ __forceinline__ f32x4 mfma16x16x32(x8 a, x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  // D[16x16] += A[16x16] B[16x16]
+  static __device__ __forceinline__ f32x4 mfma16x16x16(x4 a, x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  // D[32x32] += A[32x16] B[16x32]
+  static __device__ __forceinline__ f32x16 mfma32x32x16(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<bf16> {
+  using x4 = bf16x4;
+  using x8 = bf16x8;
+  static __device__ __forceinline__ float to_f(bf16 v) { return static_cast<float>(v); }
+  // Round to nearest even (v_cvt_pk_bf16_f32).
+  static __device__ __forceinline__ bf16 from_f(float v) { return static_cast<bf16>(v); }
+  static __device__ __forceinline__ f32x4 mfma16x16x32(x8 a, x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16x16x16(x4 a, x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4v, a),
+                                                     __builtin_bit_cast(i16x4v, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32x32x16(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Validates vaa_attn_params.dtype.
+inline bool valid_dtype(int32_t dt) { return dt == VAA_DTYPE_F16 || dt == VAA_DTYPE_BF16; }
 
 // 16-byte global load / store through a generic pointer.
 __device__ __forceinline__ u32x4 ld16(const void* p) {

@@ -211,6 +211,8 @@ extern "C" int vaa_kv_write_slots(const vaa_attn_params* p, uint16_t* key_cache,
                                   const uint16_t* new_values, int num_tokens,
                                   void* stream) {
   if (!p) return fail(VAA_ERR_INVALID_ARG, "vaa_kv_write_slots: null params");
+  if (!valid_dtype(p->dtype))  // a 16-bit copy either way
+    return fail(VAA_ERR_UNSUPPORTED, "vaa_kv_write_slots: dtype=%d", p->dtype);
   int st = check_common(p->num_kv_heads, p->head_size, key_cache, value_cache,
                         new_keys, new_values, "vaa_kv_write_slots", num_tokens);
   if (st) return st;
@@ -246,6 +248,8 @@ extern "C" int vaa_kv_write_decode(const vaa_attn_params* p, uint16_t* key_cache
                                    const uint16_t* new_keys,
                                    const uint16_t* new_values, void* stream) {
   if (!p) return fail(VAA_ERR_INVALID_ARG, "vaa_kv_write_decode: null params");
+  if (!valid_dtype(p->dtype))
+    return fail(VAA_ERR_UNSUPPORTED, "vaa_kv_write_decode: dtype=%d", p->dtype);
   int st = check_common(p->num_kv_heads, p->head_size, key_cache, value_cache,
                         new_keys, new_values, "vaa_kv_write_decode", p->num_seqs);
   if (st) return st;

@@ -45,6 +45,8 @@ namespace {
 constexpr int kWaves = 8;   // waves per workgroup
 constexpr int kTile = 16;   // tokens per MFMA tile
 
+// Tensors are raw 16-bit storage; the kernels' element type T (fp16 or bf16)
+// gives the values their meaning.
 struct DecodeArgs {
   const f16* q;
   f16* kc;
@@ -132,9 +134,9 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
 
 // One tile of math.  valid = number of real tokens in the tile (16 for every
 // tile but the sequence's last one; 0 for an invalid block).
-template <int D>
+template <int D, typename T>
 __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
-                                          const u32x4* qb, f16* vt, int valid, int g,
+                                          const u32x4* qb, T* vt, int valid, int g,
                                           float scale_log2, float& m_run, float& l_part,
                                           f32x4* acc) {
   using C = Cfg<D>;
@@ -149,9 +151,8 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
   f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < C::NS; ++s) {
-    s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, t.k[s]),
-                                                __builtin_bit_cast(f16x8, qb[s]), s4,
-                                                0, 0, 0);
+    s4 = Elem<T>::mfma16x16x32(__builtin_bit_cast(typename Elem<T>::x8, t.k[s]),
+                               __builtin_bit_cast(typename Elem<T>::x8, qb[s]), s4);
   }
   // Online softmax in the log2 domain; lane = head, tokens 4g..4g+3.
   float x[4];
@@ -172,19 +173,19 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
     m_run = m_new;
   }
   const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
-  f16x4 ph;
+  typename Elem<T>::x4 ph;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    ph[r] = f2h(fast_exp2(x[r] - m_sub));
-    l_part += h2f(ph[r]);
+    ph[r] = Elem<T>::from_f(fast_exp2(x[r] - m_sub));
+    l_part += Elem<T>::to_f(ph[r]);
   }
   // O^T += V^T P^T; lane reads V[4g+r][16dt + c16] from LDS.
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt) {
-    f16x4 va;
+    typename Elem<T>::x4 va;
 #pragma unroll
     for (int r = 0; r < 4; ++r) va[r] = vt[m.rbase[r] + (((2 * dt) ^ m.rsw[r]) << 3)];
-    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc[dt], 0, 0, 0);
+    acc[dt] = Elem<T>::mfma16x16x16(va, ph, acc[dt]);
   }
 }
 
@@ -200,7 +201,7 @@ struct RangeOut {
 // positions: each wave streams a contiguous run of tiles, then the waves
 // combine through LDS.  smem is reused on return only after the trailing
 // barrier, so a workgroup may call this repeatedly.
-template <int D>
+template <int D, typename T>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int L, bool fused, int t0, int t1,
                                              const RangeOut& ro, bool trailing_barrier) {
@@ -245,7 +246,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     for (int s = 0; s < C::NS; ++s) qb[s] = hv ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  f16* vt = reinterpret_cast<f16*>(smem) + wave * (kTile * D);
+  T* vt = reinterpret_cast<T*>(smem) + wave * (kTile * D);
   float m_run = -INFINITY, l_part = 0.f;
   f32x4 acc[C::NDT];
 #pragma unroll
@@ -272,19 +273,19 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     for (; j + 3 <= ce; j += 3) {
       p2 = window_block(a, vals, blk0, min(j + 2, jl));
       issue_tile<D>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
-      tile_math<D>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
+      tile_math<D, T>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
       p0 = window_block(a, vals, blk0, min(j + 3, jl));
       issue_tile<D>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
-      tile_math<D>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
+      tile_math<D, T>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
       p1 = window_block(a, vals, blk0, min(j + 4, jl));
       issue_tile<D>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
-      tile_math<D>(m, r2, qb, vt, valid_of(p2), g, a.scale_log2, m_run, l_part, acc);
+      tile_math<D, T>(m, r2, qb, vt, valid_of(p2), g, a.scale_log2, m_run, l_part, acc);
     }
     // Remainder (0..2 tiles): r0 holds tile j, r1 tile j+1.
     if (j < ce) {
-      tile_math<D>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
+      tile_math<D, T>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
       if (j + 1 < ce)
-        tile_math<D>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
+        tile_math<D, T>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
     }
     cb = ce;
   }
@@ -323,7 +324,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
       t.v[i] = ld16(vp);
       if (mine) st16(vb + m.voff[i], t.v[i]);
     }
-    tile_math<D>(m, t, qb, vt, valid, g, a.scale_log2, m_run, l_part, acc);
+    tile_math<D, T>(m, t, qb, vt, valid, g, a.scale_log2, m_run, l_part, acc);
   }
 
   // Sum over the four token groups of this head.
@@ -369,7 +370,8 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     }
     if (ro.whole) {
       const int qh = kvh * G + h;
-      a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
+      reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
+          Elem<T>::from_f(den > 0.f ? num / den : 0.f);
     } else {
       const int64_t row = ro.prow0 + h * ro.prow_step;
       a.ws_acc[row * D + d] = num;
@@ -398,7 +400,7 @@ __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int seq) {
 }
 
 // Fixed partitions: grid (partition, kv_head, seq).
-template <int D>
+template <int D, typename T>
 __global__ void __launch_bounds__(kWaves* kWave)
 paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -420,7 +422,7 @@ paged_decode_kernel(DecodeArgs a) {
   ro.whole = (n_parts == 1);
   ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + kvh * G) * a.max_parts + part;
   ro.prow_step = a.max_parts;
-  decode_range<D>(a, smem, seq, kvh, L, a.new_k != nullptr && Lorig == L, t0, t1, ro, false);
+  decode_range<D, T>(a, smem, seq, kvh, L, a.new_k != nullptr && Lorig == L, t0, t1, ro, false);
 }
 
 // Balanced split: the tiles of all sequences (for one kv head) are laid end
@@ -466,7 +468,7 @@ __device__ __forceinline__ void tile_prefix(const DecodeArgs& a, int* starts, in
   __syncthreads();
 }
 
-template <int D>
+template <int D, typename T>
 __global__ void __launch_bounds__(kWaves* kWave)
 paged_decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -500,7 +502,7 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(kvh) * (nc + B) + c + seq) * G;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D>(a, smem, seq, kvh, L, a.new_k != nullptr && a.seq_lens[seq] == L, t0, t1,
+    decode_range<D, T>(a, smem, seq, kvh, L, a.new_k != nullptr && a.seq_lens[seq] == L, t0, t1,
                     ro, true);
     pos = s0 + t1;
   }
@@ -510,14 +512,14 @@ paged_decode_balanced_kernel(DecodeArgs a) {
 // starts[seq]/per .. (starts[seq+1]-1)/per of its kv head; when that is one
 // workgroup the decode kernel wrote the row already.  Rows of empty
 // sequences are zeroed here.
-template <int D>
+template <int D, typename T>
 __global__ void __launch_bounds__(D)
 paged_decode_merge_balanced_kernel(DecodeArgs a) {
   const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
   const int G = a.G, B = a.num_seqs, nc = a.max_parts;
   const int L = clamped_len(a, seq);
   if (L <= 0) {
-    a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(0.f);
+    a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(0.f);  // zero bits in either type
     return;
   }
   const int per = a.ws_hdr[0];
@@ -541,12 +543,13 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
       den += sc * lp;
     }
   }
-  a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
+  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
+      Elem<T>::from_f(den > 0.f ? num / den : 0.f);
 }
 
 // Second pass for split sequences:
 //   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p.
-template <int D>
+template <int D, typename T>
 __global__ void __launch_bounds__(D)
 paged_decode_merge_kernel(DecodeArgs a) {
   const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
@@ -572,7 +575,8 @@ paged_decode_merge_kernel(DecodeArgs a) {
       den += sc * lp;
     }
   }
-  a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(den > 0.f ? num / den : 0.f);
+  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
+      Elem<T>::from_f(den > 0.f ? num / den : 0.f);
 }
 
 int g_num_cus = 0;
@@ -667,6 +671,9 @@ int check_params(const vaa_attn_params* p, const char* what) {
       p->queries_per_kv != p->num_query_heads / p->num_kv_heads)
     return fail(VAA_ERR_INVALID_ARG, "%s: heads %d/%d, queries_per_kv=%d", what,
                 p->num_query_heads, p->num_kv_heads, p->queries_per_kv);
+  if (!valid_dtype(p->dtype))
+    return fail(VAA_ERR_UNSUPPORTED, "%s: dtype=%d (VAA_DTYPE_F16 or VAA_DTYPE_BF16)", what,
+                p->dtype);
   if (p->queries_per_kv > 16)
     return fail(VAA_ERR_UNSUPPORTED, "%s: queries_per_kv=%d > 16", what,
                 p->queries_per_kv);
@@ -689,7 +696,7 @@ int check_params(const vaa_attn_params* p, const char* what) {
   return VAA_OK;
 }
 
-template <int D>
+template <int D, typename T>
 int launch_decode(const DecodeArgs& a0, bool balanced, hipStream_t stream) {
   DecodeArgs a = a0;
   const size_t lds_tiles = static_cast<size_t>(kWaves) * kTile * D * sizeof(f16);
@@ -699,19 +706,19 @@ int launch_decode(const DecodeArgs& a0, bool balanced, hipStream_t stream) {
   if (balanced) {
     a.lds_main = static_cast<int>((lds + 15) / 16 * 16);
     const size_t lds_b = a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kWaves) * sizeof(int);
-    hipLaunchKernelGGL(paged_decode_balanced_kernel<D>, dim3(a.max_parts, a.num_kv_heads),
+    hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T>), dim3(a.max_parts, a.num_kv_heads),
                        dim3(kWaves * kWave), lds_b, stream, a);
     int st = check_launch("paged_decode_balanced_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(paged_decode_merge_balanced_kernel<D>, dim3(a.num_q_heads, a.num_seqs),
+    hipLaunchKernelGGL((paged_decode_merge_balanced_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs),
                        dim3(D), 0, stream, a);
     return check_launch("paged_decode_merge_balanced_kernel");
   }
   dim3 grid(a.max_parts, a.num_kv_heads, a.num_seqs);
-  hipLaunchKernelGGL(paged_decode_kernel<D>, grid, dim3(kWaves * kWave), lds, stream, a);
+  hipLaunchKernelGGL((paged_decode_kernel<D, T>), grid, dim3(kWaves * kWave), lds, stream, a);
   int st = check_launch("paged_decode_kernel");
   if (st || a.max_parts <= 1) return st;
-  hipLaunchKernelGGL(paged_decode_merge_kernel<D>, dim3(a.num_q_heads, a.num_seqs), dim3(D),
+  hipLaunchKernelGGL((paged_decode_merge_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs), dim3(D),
                      0, stream, a);
   return check_launch("paged_decode_merge_kernel");
 }
@@ -806,11 +813,16 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   a.n_st = p->new_kv_stride_token; a.n_sh = p->new_kv_stride_head;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bf = p->dtype == VAA_DTYPE_BF16;
   switch (p->head_size) {
-    case 32: return launch_decode<32>(a, sp.balanced, s);
-    case 64: return launch_decode<64>(a, sp.balanced, s);
-    case 96: return launch_decode<96>(a, sp.balanced, s);
-    case 128: return launch_decode<128>(a, sp.balanced, s);
+    case 32: return bf ? launch_decode<32, bf16>(a, sp.balanced, s)
+                       : launch_decode<32, f16>(a, sp.balanced, s);
+    case 64: return bf ? launch_decode<64, bf16>(a, sp.balanced, s)
+                       : launch_decode<64, f16>(a, sp.balanced, s);
+    case 96: return bf ? launch_decode<96, bf16>(a, sp.balanced, s)
+                       : launch_decode<96, f16>(a, sp.balanced, s);
+    case 128: return bf ? launch_decode<128, bf16>(a, sp.balanced, s)
+                        : launch_decode<128, f16>(a, sp.balanced, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
 }

@@ -99,10 +99,11 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return v;
 }
 
-__device__ __forceinline__ f16x4 lds_tr4(const f16* p) {
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::x4 lds_tr4(const f16* p) {
   const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) i16x4*)(p));
-  return __builtin_bit_cast(f16x4, r);
+  return __builtin_bit_cast(typename Elem<T>::x4, r);
 }
 
 // s_waitcnt vmcnt(0) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
@@ -227,7 +228,7 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
 // One 64-key tile for this wave's 32 query rows: S^T = K Q^T as two
 // independent 32-key MFMA row blocks, online softmax over both, then
 // O^T += V^T P^T over four 16-key groups.
-template <int D>
+template <int D, typename T>
 __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, const f16* vt,
                                           int key0, int lim, int hb, const Lanes<D>& L,
                                           const u32x4 (&qb)[PCfg<D>::NK], float& m_run,
@@ -247,9 +248,9 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
     for (int j = 0; j < 2; ++j) {
       const u32x4 kA =
           *reinterpret_cast<const u32x4*>(kbytes + L.kaddr[s2] + 32 * j * C::ROWB);
-      sacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kA),
-                                                       __builtin_bit_cast(f16x8, qb[s2]),
-                                                       sacc[j], 0, 0, 0);
+      sacc[j] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, kA),
+                                      __builtin_bit_cast(typename Elem<T>::x8, qb[s2]),
+                                      sacc[j]);
     }
   }
   // Lane holds keys 32j + 8(r/4) + 4hb + r%4 for query qj.  The mask is only
@@ -282,13 +283,13 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
   }
   const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
   // pb[g]: B operand for 16-key group g (keys 16g + 8(i/4) + 4hb + i%4).
-  f16x8 pb[4];
+  typename Elem<T>::x8 pb[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float p = fast_exp2(fmaf(sacc[j][r], a.scale_log2, -m_sub));
-      pb[2 * j + (r >> 3)][r & 7] = f2h(p);
+      pb[2 * j + (r >> 3)][r & 7] = Elem<T>::from_f(p);
       l_part += p;
     }
   // O^T += V^T P^T; V^T for key group g comes from the transposing LDS read.
@@ -297,15 +298,15 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f16* vp = reinterpret_cast<const f16*>(vbytes + L.vaddr[dt] + 16 * g * C::ROWB);
-      const f16x4 lo = lds_tr4(vp);
-      const f16x4 hi = lds_tr4(vp + 8 * D);
-      const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[g], acc[dt], 0, 0, 0);
+      const typename Elem<T>::x4 lo = lds_tr4<T>(vp);
+      const typename Elem<T>::x4 hi = lds_tr4<T>(vp + 8 * D);
+      const typename Elem<T>::x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      acc[dt] = Elem<T>::mfma32x32x16(va, pb[g], acc[dt]);
     }
   }
 }
 
-template <int D>
+template <int D, typename T>
 __global__ void __launch_bounds__(kThreadsP) __attribute__((amdgpu_waves_per_eu(2, 2)))
 paged_prefill_kernel(PrefillArgs a) {
   using C = PCfg<D>;
@@ -405,14 +406,14 @@ paged_prefill_kernel(PrefillArgs a) {
       if (kt + 1 < n_kt)
         tile_fetch<D>(a, bts, kvh, (kt + 1) * kKT, kv_len, lim, wave, lane, L, win, aborted,
                       k1s, v1s);
-      if (math) tile_math<D>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
+      if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
       wait_all();
       __builtin_amdgcn_s_barrier();
       if (kt + 1 >= n_kt) break;
       if (kt + 2 < n_kt)
         tile_fetch<D>(a, bts, kvh, (kt + 2) * kKT, kv_len, lim, wave, lane, L, win, aborted,
                       k0s, v0s);
-      if (math) tile_math<D>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
+      if (math) tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
       wait_all();
       __builtin_amdgcn_s_barrier();
     }
@@ -428,16 +429,16 @@ paged_prefill_kernel(PrefillArgs a) {
   for (int dt = 0; dt < C::NDT; ++dt) {
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
-      f16x4 o;
+      typename Elem<T>::x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = f2h(acc[dt][4 * rg + i] * inv);
+      for (int i = 0; i < 4; ++i) o[i] = Elem<T>::from_f(acc[dt][4 * rg + i] * inv);
       const int d = 32 * dt + 8 * rg + 4 * hb;
-      *reinterpret_cast<f16x4*>(op + d) = o;
+      *reinterpret_cast<typename Elem<T>::x4*>(op + d) = o;
     }
   }
 }
 
-template <int D>
+template <int D, typename T>
 int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   const int per_wg = kQT * a.subtiles;
   const int gx = (a.num_tokens + per_wg - 1) / per_wg, gy = num_kv_heads * a.head_chunks;
@@ -448,7 +449,7 @@ int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   b.tiles_y = gy;
   b.padded_tiles = padded;
   dim3 grid(gx, (padded + gx - 1) / gx);
-  hipLaunchKernelGGL(paged_prefill_kernel<D>, grid, dim3(kThreadsP), 0, stream, b);
+  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), grid, dim3(kThreadsP), 0, stream, b);
   return check_launch("paged_prefill_kernel");
 }
 
@@ -482,6 +483,8 @@ extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
     return fail(VAA_ERR_UNSUPPORTED,
                 "vaa_paged_attention_prefill: block_size=%d is not a multiple of 16",
                 p->block_size);
+  if (!valid_dtype(p->dtype))
+    return fail(VAA_ERR_UNSUPPORTED, "vaa_paged_attention_prefill: dtype=%d", p->dtype);
   if (num_tokens == 0) return VAA_OK;
   if (!query || !key_cache || !value_cache || !block_table || !token_to_seq ||
       !positions || !output)
@@ -531,11 +534,16 @@ extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
   a.q_st = p->q_stride_token; a.q_sh = p->q_stride_head;
   a.o_st = p->o_stride_token; a.o_sh = p->o_stride_head;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bf = p->dtype == VAA_DTYPE_BF16;
   switch (p->head_size) {
-    case 32: return launch_prefill<32>(a, p->num_kv_heads, s);
-    case 64: return launch_prefill<64>(a, p->num_kv_heads, s);
-    case 96: return launch_prefill<96>(a, p->num_kv_heads, s);
-    case 128: return launch_prefill<128>(a, p->num_kv_heads, s);
+    case 32: return bf ? launch_prefill<32, bf16>(a, p->num_kv_heads, s)
+                       : launch_prefill<32, f16>(a, p->num_kv_heads, s);
+    case 64: return bf ? launch_prefill<64, bf16>(a, p->num_kv_heads, s)
+                       : launch_prefill<64, f16>(a, p->num_kv_heads, s);
+    case 96: return bf ? launch_prefill<96, bf16>(a, p->num_kv_heads, s)
+                       : launch_prefill<96, f16>(a, p->num_kv_heads, s);
+    case 128: return bf ? launch_prefill<128, bf16>(a, p->num_kv_heads, s)
+                        : launch_prefill<128, f16>(a, p->num_kv_heads, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
 }

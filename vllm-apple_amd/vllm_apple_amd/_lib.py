@@ -31,6 +31,11 @@ VAA_INDEX_I64 = 1
 # partition_size value asking decode to split by the actual lengths on the device.
 VAA_PARTITION_BALANCED = -1
 
+# Element types of caches, queries, new K/V and outputs (vaa_attn_params.dtype).
+VAA_DTYPE_F16 = 0
+VAA_DTYPE_BF16 = 1
+ABI_VERSION = 2
+
 
 class NativeLibraryError(RuntimeError):
     """The HIP library could not be loaded (not built, or wrong platform)."""
@@ -67,6 +72,7 @@ class VaaAttnParams(ctypes.Structure):
         ("o_stride_head", ctypes.c_int64),
         ("new_kv_stride_token", ctypes.c_int64),
         ("new_kv_stride_head", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
     ]
 
 
@@ -123,7 +129,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.vaa_abi_version() != 1:
+        if lib.vaa_abi_version() != ABI_VERSION:
             raise NativeLibraryError("ABI version mismatch")
         _lib = lib
         return lib

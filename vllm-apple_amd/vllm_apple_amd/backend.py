@@ -223,13 +223,14 @@ class HipAttentionImpl(AttentionImpl):
 
     # ------------------------------------------------------------------ cache
     def _caches(self, kv_cache: torch.Tensor) -> tuple:
-        """(key_cache, value_cache) in the vLLM layout [nb, bs, KV, D], fp16.
+        """(key_cache, value_cache) in the vLLM layout [nb, bs, KV, D].
 
-        An fp16 kv_cache is used in place.  For any other cache dtype (bf16
-        models) a same-shaped fp16 cache is kept per layer, as the Metal
-        backend keeps its own fp16 cache (metal_attn.py:654-660).
+        An fp16 or bf16 kv_cache is used in place: the kernels take both
+        element types, so bf16 models need neither the fp16 copy of the cache
+        the Metal backend keeps (metal_attn.py:654-660) nor conversions.  Any
+        other cache dtype gets a same-shaped fp16 cache kept per layer.
         """
-        if kv_cache.dtype == torch.float16:
+        if kv_cache.dtype in kernels.ATTN_DTYPES:
             return kv_cache[0], kv_cache[1]
         if self._shadow is None or self._shadow.shape != kv_cache.shape:
             self._shadow = torch.zeros(kv_cache.shape, dtype=torch.float16,
@@ -250,14 +251,20 @@ class HipAttentionImpl(AttentionImpl):
         if attn_metadata is None:  # warm-up / profiling
             return output
 
-        # bf16 activations run through the fp16 kernels (metal_attn.py:609-620).
+        # The kernels run in the cache's element type (fp16 or bf16).  Only
+        # activations of another type are converted, as the Metal backend
+        # converts bf16 for its fp16 kernels (metal_attn.py:609-620).
         original_output = output
-        conv = query.dtype == torch.bfloat16
+        if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
+            work_dt = query.dtype if query.dtype in kernels.ATTN_DTYPES else torch.float16
+        else:
+            work_dt = kv_cache.dtype if kv_cache.dtype in kernels.ATTN_DTYPES else torch.float16
+        conv = query.dtype != work_dt
         if conv:
-            query = query.to(torch.float16)
-            key = key.to(torch.float16) if key is not None else None
-            value = value.to(torch.float16) if value is not None else None
-            output = torch.empty(output.shape, dtype=torch.float16, device=output.device)
+            query = query.to(work_dt)
+            key = key.to(work_dt) if key is not None else None
+            value = value.to(work_dt) if value is not None else None
+            output = torch.empty(output.shape, dtype=work_dt, device=output.device)
 
         n = attn_metadata.num_actual_tokens
         if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
@@ -325,7 +332,7 @@ class HipAttentionImpl(AttentionImpl):
                 pos.append(i if causal else n - 1)
         dev = query.device
         kv = key.shape[1]
-        kc = torch.empty((total, bs, kv, self.head_size), dtype=torch.float16, device=dev)
+        kc = torch.empty((total, bs, kv, self.head_size), dtype=query.dtype, device=dev)
         vc = torch.empty_like(kc)
         slot_t = torch.tensor(slots, dtype=torch.int64).to(dev, non_blocking=True)
         bt_t = torch.tensor(bt, dtype=torch.int32).to(dev, non_blocking=True)

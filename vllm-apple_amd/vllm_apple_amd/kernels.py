@@ -40,6 +40,19 @@ def _require_dtype(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
 
 
+# 16-bit element types the attention entry points take (vaa_attn_params.dtype).
+ATTN_DTYPES = {torch.float16: _lib.VAA_DTYPE_F16, torch.bfloat16: _lib.VAA_DTYPE_BF16}
+
+
+def _attn_dtype(**named: torch.Tensor | None) -> torch.dtype:
+    """The one element type (fp16 or bf16) shared by all the given tensors."""
+    dtypes = {n: t.dtype for n, t in named.items() if t is not None}
+    kinds = set(dtypes.values())
+    if len(kinds) != 1 or next(iter(kinds)) not in ATTN_DTYPES:
+        raise ValueError(f"tensors must all be float16 or all bfloat16, got {dtypes}")
+    return next(iter(kinds))
+
+
 @dataclass(frozen=True)
 class CacheStrides:
     num_blocks: int
@@ -82,7 +95,11 @@ def make_params(*, key_cache: torch.Tensor, value_cache: torch.Tensor, layout: s
     if num_query_heads % ks.num_kv_heads != 0:
         raise ValueError(
             f"num_query_heads={num_query_heads} not a multiple of num_kv_heads={ks.num_kv_heads}")
+    if key_cache.dtype != value_cache.dtype or key_cache.dtype not in ATTN_DTYPES:
+        raise ValueError(f"caches must both be float16 or bfloat16, got "
+                         f"{key_cache.dtype}/{value_cache.dtype}")
     p = _lib.VaaAttnParams()
+    p.dtype = ATTN_DTYPES[key_cache.dtype]
     p.scale = float(scale)
     p.num_seqs = int(num_seqs)
     p.max_seq_len = int(max_seq_len)
@@ -114,13 +131,12 @@ def kv_write_slots(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tens
                    layout: str = "kernel", stream=None) -> None:
     """cache[slot // bs, :, slot % bs] = key/value[t] for every slot >= 0.
 
-    key/value: [num_tokens, num_kv_heads, head_size] fp16 (any token/head
+    key/value: [num_tokens, num_kv_heads, head_size] fp16 or bf16 (any token/head
     strides with a contiguous last dim); slot_mapping: int32 or int64
     [num_tokens].  Mirrors kv_write.py:118-156 and base_attn.py:308-342.
     """
     _require_gpu(key, value, key_cache, value_cache, slot_mapping)
-    for t, n in ((key, "key"), (value, "value"), (key_cache, "key_cache"), (value_cache, "value_cache")):
-        _require_dtype(t, torch.float16, n)
+    _attn_dtype(key=key, value=value, key_cache=key_cache, value_cache=value_cache)
     if key.stride() != value.stride() or key.shape != value.shape:
         raise ValueError("key and value must have identical shapes and strides")
     if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous():
@@ -143,6 +159,8 @@ def kv_write_decode(new_keys: torch.Tensor, new_values: torch.Tensor, key_cache:
                     seq_lens: torch.Tensor, *, layout: str = "kernel", stream=None) -> None:
     """Write each sequence's new token at position seq_lens[s]-1 (kv_write.py:66-114)."""
     _require_gpu(new_keys, new_values, key_cache, value_cache, block_table, seq_lens)
+    _attn_dtype(new_keys=new_keys, new_values=new_values, key_cache=key_cache,
+                value_cache=value_cache)
     _check_tables(block_table, seq_lens)
     if new_keys.stride() != new_values.stride() or new_keys.shape != new_values.shape:
         raise ValueError("new_keys and new_values must have identical shapes and strides")
@@ -299,7 +317,8 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
                  seq_lens_host=None, stream=None) -> torch.Tensor:
     """Paged GQA decode attention, one query token per sequence.
 
-    query [num_seqs, H, D] fp16; returns/fills output [num_seqs, H, D].  With
+    query [num_seqs, H, D] fp16 or bf16 (the caches', new K/V's and output's
+    type too); returns/fills output [num_seqs, H, D].  With
     new_keys/new_values ([num_seqs, KV, D]) the token at position
     seq_lens[s]-1 is written to the cache by the same launch (fused KV write).
     max_seq_len must bound seq_lens (it sizes the split-K grid).  With
@@ -308,11 +327,12 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
     partition_size PARTITION_BALANCED splits by the lengths on the device.
     """
     _require_gpu(query, key_cache, value_cache, block_table, seq_lens, output, new_keys, new_values)
-    _require_dtype(query, torch.float16, "query")
+    dt = _attn_dtype(query=query, key_cache=key_cache, value_cache=value_cache, output=output,
+                     new_keys=new_keys, new_values=new_values)
     _check_tables(block_table, seq_lens)
     num_seqs = seq_lens.numel()
     if output is None:
-        output = torch.empty(query.shape, dtype=torch.float16, device=query.device)
+        output = torch.empty(query.shape, dtype=dt, device=query.device)
     if query.shape[0] < num_seqs or output.shape[0] < num_seqs:
         raise ValueError("query/output have fewer rows than sequences")
     if (new_keys is None) != (new_values is None):
@@ -349,12 +369,13 @@ def paged_prefill(query: torch.Tensor, key_cache: torch.Tensor, value_cache: tor
                   output: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Chunked-prefill attention: token t attends to cache positions [0, positions[t]].
 
-    query [num_tokens, H, D] fp16; the tokens' own K/V must already be cached.
+    query [num_tokens, H, D] fp16 or bf16, as the caches and output; the
+    tokens' own K/V must already be cached.
     Rows the reference kernel leaves unwritten (invalid sequence, negative
     position, context past the block table, invalid block) stay untouched.
     """
     _require_gpu(query, key_cache, value_cache, block_table, token_to_seq, positions, output)
-    _require_dtype(query, torch.float16, "query")
+    dt = _attn_dtype(query=query, key_cache=key_cache, value_cache=value_cache, output=output)
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or not block_table.is_contiguous():
         raise ValueError("block_table must be a contiguous int32 2-D tensor")
     for t, n in ((token_to_seq, "token_to_seq"), (positions, "positions")):
@@ -364,7 +385,7 @@ def paged_prefill(query: torch.Tensor, key_cache: torch.Tensor, value_cache: tor
     if token_to_seq.numel() < num_tokens or positions.numel() < num_tokens:
         raise ValueError("token_to_seq/positions shorter than query")
     if output is None:
-        output = torch.zeros(query.shape, dtype=torch.float16, device=query.device)
+        output = torch.zeros(query.shape, dtype=dt, device=query.device)
     p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
                     num_query_heads=query.shape[1], scale=scale, num_seqs=block_table.shape[0],
                     max_blocks_per_seq=block_table.shape[1], query=query, output=output)
