@@ -46,7 +46,7 @@ def parse() -> argparse.Namespace:
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="headline",
-                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "all"],
+                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C2bf16", "all"],
                     help="headline = the contract line; the others print one JSON line per "
                          "BASELINE config (measurement record, not the driver's metric)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -258,6 +258,11 @@ def wl_c3(args) -> dict:
                                                 b.token_to_seq, b.positions, scale=b.scale,
                                                 output=out), args.steps, args.warmup)
     fl = _prefill_flops(b)
+    bb = workloads.c3_prefill(device=torch.device("cuda:0"), dtype=torch.bfloat16)
+    out_b = torch.empty_like(bb.query)
+    t_bf = _timed(lambda: kernels.paged_prefill(bb.query, bb.k_cache, bb.v_cache, bb.block_table,
+                                                bb.token_to_seq, bb.positions, scale=bb.scale,
+                                                output=out_b), args.steps, args.warmup)
     T = b.query.shape[0]
     kv_bytes = 2 * 2 * T * b.num_kv_heads * b.head_size * 2 + T * 8
     return {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
@@ -265,7 +270,9 @@ def wl_c3(args) -> dict:
             "kv_write_gb_s": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
             "prefill_ms": round(t_at, 5), "flops": fl,
             "tflop_s": round(fl / (t_at * 1e-3) / 1e12, 1),
-            "mfma_util_pct": round(100 * fl / (t_at * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2)}
+            "mfma_util_pct": round(100 * fl / (t_at * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2),
+            "bf16_prefill_ms": round(t_bf, 5),
+            "bf16_tflop_s": round(fl / (t_bf * 1e-3) / 1e12, 1)}
 
 
 def wl_c5(args) -> dict:
@@ -317,7 +324,20 @@ def wl_c5(args) -> dict:
     return rec
 
 
-WORKLOADS = {"C1": wl_c1, "C2u": wl_c2u, "C3": wl_c3, "C4": wl_c4, "C5": wl_c5}
+def wl_c2bf16(args) -> dict:
+    """The headline shape (B=32, all contexts 8192) with a bf16 cache and bf16
+    activations: bf16 models run through the same kernels without an fp16 copy."""
+    import torch
+
+    from vllm_apple_amd import workloads
+
+    b = workloads.c2_decode(device=torch.device("cuda:0"), fixed_len=8192,
+                            dtype=torch.bfloat16)
+    return _decode_record("C2-bf16", b, args, 0, "headline shape in bf16 (extension)")
+
+
+WORKLOADS = {"C1": wl_c1, "C2u": wl_c2u, "C3": wl_c3, "C4": wl_c4, "C5": wl_c5,
+             "C2bf16": wl_c2bf16}
 
 
 def main() -> int:
@@ -336,7 +356,8 @@ def main() -> int:
 
     _lib.load()
     if args.workload != "headline":
-        names = ["C1", "C2u", "C3", "C4", "C5"] if args.workload == "all" else [args.workload]
+        names = (["C1", "C2u", "C3", "C4", "C5", "C2bf16"] if args.workload == "all"
+                 else [args.workload])
         for name in names:
             print(json.dumps(WORKLOADS[name](args)), flush=True)
         return 0

@@ -80,15 +80,17 @@ def _gen(device, seed: int) -> torch.Generator:
     return g
 
 
-def _randn(shape, g, device, std: float = 1.0, mean: float = 0.0) -> torch.Tensor:
+def _randn(shape, g, device, std: float = 1.0, mean: float = 0.0,
+           dtype: torch.dtype = torch.float16) -> torch.Tensor:
     t = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
     if std != 1.0 or mean != 0.0:
         t = t * std + mean
-    return t.to(torch.float16)
+    return t.to(dtype)
 
 
 def _paged_batch(*, device, g, H, KV, D, ctx_lens, new_per_seq, pool_blocks,
-                 max_blocks=None, scale=None, bs=BLOCK_SIZE) -> PagedBatch:
+                 max_blocks=None, scale=None, bs=BLOCK_SIZE,
+                 dtype: torch.dtype = torch.float16) -> PagedBatch:
     """Caches + block tables for sequences of total lengths ctx_lens, whose last
     new_per_seq[s] tokens are this step's queries (positions L-n .. L-1)."""
     S = len(ctx_lens)
@@ -104,12 +106,12 @@ def _paged_batch(*, device, g, H, KV, D, ctx_lens, new_per_seq, pool_blocks,
     for s, n in enumerate(nblk):
         bt[s, :n] = perm[off:off + n]
         off += n
-    k_cache = _randn((pool_blocks, KV, bs, D), g, device)
-    v_cache = _randn((pool_blocks, KV, bs, D), g, device)
+    k_cache = _randn((pool_blocks, KV, bs, D), g, device, dtype=dtype)
+    v_cache = _randn((pool_blocks, KV, bs, D), g, device, dtype=dtype)
     T = sum(new_per_seq)
-    query = _randn((T, H, D), g, device)
-    new_k = _randn((T, KV, D), g, device)
-    new_v = _randn((T, KV, D), g, device)
+    query = _randn((T, H, D), g, device, dtype=dtype)
+    new_k = _randn((T, KV, D), g, device, dtype=dtype)
+    new_v = _randn((T, KV, D), g, device, dtype=dtype)
     qsl = [0]
     tok, pos = [], []
     for s, (L, n) in enumerate(zip(ctx_lens, new_per_seq)):
@@ -146,21 +148,23 @@ def c1_decode(device="cpu", seed: int | None = None) -> PagedBatch:
 
 
 def c2_decode(device="cpu", seed: int | None = None, fixed_len: int | None = None,
-              batch: int = 32) -> PagedBatch:
+              batch: int = 32, dtype: torch.dtype = torch.float16) -> PagedBatch:
     g = _gen(device, seed or SEEDS["C2"])
     lens = [fixed_len] * batch if fixed_len else _uniform_int(g, 1024, 8192, batch, device)
     pool = math.ceil(300_000 / BLOCK_SIZE)
     return _paged_batch(device=device, g=g, H=32, KV=8, D=128, ctx_lens=lens,
-                        new_per_seq=[1] * batch, pool_blocks=pool, max_blocks=8192 // BLOCK_SIZE)
+                        new_per_seq=[1] * batch, pool_blocks=pool, max_blocks=8192 // BLOCK_SIZE,
+                        dtype=dtype)
 
 
 def c3_prefill(device="cpu", seed: int | None = None, cached: int = 2048, chunk: int = 512,
-               num_seqs: int = 4) -> PagedBatch:
+               num_seqs: int = 4, dtype: torch.dtype = torch.float16) -> PagedBatch:
     g = _gen(device, seed or SEEDS["C3"])
     L = cached + chunk
     nblk = (L + BLOCK_SIZE - 1) // BLOCK_SIZE
     return _paged_batch(device=device, g=g, H=32, KV=8, D=128, ctx_lens=[L] * num_seqs,
-                        new_per_seq=[chunk] * num_seqs, pool_blocks=2 * nblk * num_seqs)
+                        new_per_seq=[chunk] * num_seqs, pool_blocks=2 * nblk * num_seqs,
+                        dtype=dtype)
 
 
 def c4_long_decode(device="cpu", seed: int | None = None, batch: int = 64) -> PagedBatch:
