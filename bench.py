@@ -304,6 +304,30 @@ def wl_c5(args) -> dict:
     q2, k2 = b.query.clone(), b.new_k.clone()
     t_rope = _timed(lambda: kernels.rope_neox_(q2, k2, cos, sin, b.positions), args.steps,
                     args.warmup)
+    # QKV epilogue over the step's planar QKV views: fused (one launch) against
+    # the reference's three passes (bias add, RoPE, KV write).
+    T_, H_, KV_, D_ = T, b.num_q_heads, b.num_kv_heads, b.head_size
+    gq = torch.Generator(device=dev).manual_seed(7)
+    qkv = torch.randn(T_ * (H_ + 2 * KV_) * D_, generator=gq, device=dev).half()
+    bias = torch.randn((H_ + 2 * KV_) * D_, generator=gq, device=dev).half()
+    qv = qkv[:T_ * H_ * D_].view(T_, H_, D_)
+    kv_ = qkv[T_ * H_ * D_:T_ * (H_ + KV_) * D_].view(T_, KV_, D_)
+    vv = qkv[T_ * (H_ + KV_) * D_:].view(T_, KV_, D_)
+    t_epi = _timed(lambda: kernels.qkv_epilogue(qv, kv_, vv, b.positions, cos, sin,
+                                                b.slot_mapping, b.k_cache, b.v_cache,
+                                                bias=bias), args.steps, args.warmup)
+
+    def three_step():
+        qv.add_(bias[:H_ * D_].view(1, H_, D_))
+        kv_.add_(bias[H_ * D_:(H_ + KV_) * D_].view(1, KV_, D_))
+        vv.add_(bias[(H_ + KV_) * D_:].view(1, KV_, D_))
+        kernels.rope_neox_(qv, kv_, cos, sin, b.positions)
+        kernels.kv_write_slots(kv_, vv, b.k_cache, b.v_cache, b.slot_mapping)
+
+    t_three = _timed(three_step, args.steps, args.warmup)
+    n_qkv = qkv.numel() * 2
+    epi_bytes = 2 * n_qkv + bias.numel() * 2 + T_ * (D_ // 2) * 4 * 2 + T_ * 8 \
+        + 2 * T_ * KV_ * D_ * 2
     g, u = b.extra["gate"], b.extra["up"]
     act = torch.empty_like(g)
     t_silu = _timed(lambda: kernels.silu_mul(g, u, out=act), args.steps, args.warmup)
@@ -317,8 +341,9 @@ def wl_c5(args) -> dict:
            "attention_step_ms": round(t_attn, 5),
            "attention_decode_kv_bytes": kv_read,
            "attention_prefill_flops": 4.0 * D * H * pre_ctx}
+    rec["qkv_epilogue_three_pass_ms"] = round(t_three, 5)
     for nm, t, by in (("rmsnorm", t_norm, norm_bytes), ("rope", t_rope, rope_bytes),
-                      ("silu_mul", t_silu, silu_bytes)):
+                      ("silu_mul", t_silu, silu_bytes), ("qkv_epilogue", t_epi, epi_bytes)):
         rec[nm] = {"ms": round(t, 5), "bytes": by, "gb_s": round(by / (t * 1e-3) / 1e9, 1),
                    "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
     return rec

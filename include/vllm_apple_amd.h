@@ -288,6 +288,40 @@ int vaa_silu_mul_2d(const uint16_t* gate, const uint16_t* up, uint16_t* output,
                     int64_t rows, int64_t cols, int64_t gate_stride,
                     int64_t up_stride, int64_t output_stride, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused QKV epilogue
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Bias add + NeoX rotary embedding + KV write in one pass over the QKV
+ * projection's output.  No single counterpart in the reference; it fuses the
+ * three kernels the reference runs in turn over its planar QKV buffer
+ * (vllm_apple/engine/runner.py:919-1016): bias_add_inplace_kernel on Q, K and V
+ * (engine/ops/qkv.py:391-416, elementwise.py:252-259), rope_neox_kernel on Q
+ * and K (elementwise.py:185-239) and kv_write_prefill (kv_write.py:118-156).
+ * For token t:
+ *   q[t] <- rope(q[t] + bias_q)            in place
+ *   k[t] <- rope(k[t] + bias_k)            in place, and to the cache slot
+ *   v[t] <- v[t] + bias_v                  in place, and to the cache slot
+ * where the biased values are rounded to the 16-bit type before the rotation
+ * (the reference's half add), rope rotates the first rotary_dim elements by
+ * cos/sin_cache[positions[t]] (fp32 [max_position, rotary_dim/2]; positions
+ * outside the table are left unrotated) and the slot rule is
+ * vaa_kv_write_slots's (slot_mapping[t] < 0 or past the cache: no write).
+ * bias is [H*D | KV*D | KV*D] in the element type, or null.  query is
+ * [T, H, D] with token stride p->q_stride_token, key and value [T, KV, D]
+ * share p->new_kv_stride_token; heads are packed at stride D.  Uses
+ * p->dtype, num_query_heads, num_kv_heads, head_size, block_size, num_blocks
+ * and the k_/v_stride_* of the cache.  rotary_dim is a multiple of 16 and at
+ * most head_size.
+ */
+int vaa_qkv_epilogue(const vaa_attn_params* p, uint16_t* query, uint16_t* key,
+                     uint16_t* value, const uint16_t* bias, const float* cos_cache,
+                     const float* sin_cache, int rotary_dim, int max_position,
+                     const int32_t* positions, const void* slot_mapping,
+                     int slot_index_type, uint16_t* key_cache, uint16_t* value_cache,
+                     int num_tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

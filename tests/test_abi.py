@@ -114,3 +114,30 @@ def test_zero_sized_calls_are_noops(lib):
     assert lib.vaa_kv_write_slots(ctypes.byref(p), None, None, None, 0, None, None, 0, None) == 0
     assert lib.vaa_silu_mul(None, None, None, 0, None) == 0
     assert lib.vaa_build_token_index(None, None, 0, 0, None, None, None) == 0
+
+
+def test_dtype_and_epilogue_argument_errors(lib):
+    """dtype outside {F16, BF16} and bad epilogue shapes are refused before any launch."""
+    from vllm_apple_amd import _lib
+
+    p = _lib.VaaAttnParams()
+    p.head_size, p.block_size, p.num_kv_heads, p.num_query_heads = 128, 16, 8, 32
+    p.queries_per_kv, p.num_seqs, p.max_blocks_per_seq, p.num_blocks = 4, 1, 4, 4
+    p.dtype = 7
+    st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
+                                        None, None, None, 0, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED and "dtype=7" in _lib.last_error()
+    st = lib.vaa_kv_write_slots(ctypes.byref(p), None, None, None, 0, None, None, 1, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED
+    p.dtype = _lib.VAA_DTYPE_BF16
+    # rotary_dim not a multiple of 16
+    st = lib.vaa_qkv_epilogue(ctypes.byref(p), None, None, None, None, None, None, 24, 16,
+                              None, None, 0, None, None, 3, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED and "rotary_dim=24" in _lib.last_error()
+    # null tensors
+    st = lib.vaa_qkv_epilogue(ctypes.byref(p), None, None, None, None, None, None, 128, 16,
+                              None, None, 0, None, None, 3, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "null pointer" in _lib.last_error()
+    # zero tokens is a no-op
+    assert lib.vaa_qkv_epilogue(ctypes.byref(p), None, None, None, None, None, None, 128, 16,
+                                None, None, 0, None, None, 0, None) == 0

@@ -29,6 +29,7 @@ SOURCES = [
     "paged_prefill.hip",
     "layer_ops.hip",
     "index_ops.hip",
+    "qkv_epilogue.hip",
 ]
 
 ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")

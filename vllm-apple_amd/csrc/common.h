@@ -107,6 +107,28 @@ struct Elem<bf16> {
 // Validates vaa_attn_params.dtype.
 inline bool valid_dtype(int32_t dt) { return dt == VAA_DTYPE_F16 || dt == VAA_DTYPE_BF16; }
 
+// NeoX rotation of 8 pairs (x0[e], x1[e]) by angles with cosine c[e] and sine
+// s[e], in fp32 (elementwise.py:185-239):
+//   y0 = x0 c - x1 s,  y1 = x0 s + x1 c
+// evaluated as one rounded product and one fused multiply-add each, and the
+// fp32 results materialised (empty asm) before the caller rounds them to 16
+// bits.  Written out so the two kernels that share this (the RoPE kernel and
+// the fused QKV epilogue) round alike: otherwise the compiler may contract
+// them differently, or fold the final fma and the fp16 conversion into one
+// mixed-precision fma (v_fma_mixlo_f16, a single rounding) in one kernel and
+// not the other.
+__device__ __forceinline__ void rope_rotate8(const float* x0, const float* x1, const float* c,
+                                             const float* s, float* y0, float* y1) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float t0 = x1[e] * s[e];
+    const float t1 = x1[e] * c[e];
+    y0[e] = __builtin_fmaf(x0[e], c[e], -t0);
+    y1[e] = __builtin_fmaf(x0[e], s[e], t1);
+    asm volatile("" : "+v"(y0[e]), "+v"(y1[e]));
+  }
+}
+
 // 16-byte global load / store through a generic pointer.
 __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);

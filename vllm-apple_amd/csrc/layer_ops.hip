@@ -156,11 +156,7 @@ __global__ void __launch_bounds__(256) rope_neox_vec_kernel(RopeArgs a) {
     unpack8(ld16(x + i0), x0);
     unpack8(ld16(x + i0 + half), x1);
     float y0[8], y1[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      y0[e] = x0[e] * c[e] - x1[e] * s[e];
-      y1[e] = x0[e] * s[e] + x1[e] * c[e];
-    }
+    rope_rotate8(x0, x1, c, s, y0, y1);
     st16(x + i0, pack8(y0));
     st16(x + i0 + half, pack8(y1));
   }

@@ -497,6 +497,59 @@ def rope_neox_(query: torch.Tensor, key: torch.Tensor | None, cos_cache: torch.T
               _lib.stream_handle(stream))
 
 
+def qkv_epilogue(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                 positions: torch.Tensor, cos_cache: torch.Tensor, sin_cache: torch.Tensor,
+                 slot_mapping: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                 *, bias: torch.Tensor | None = None, rotary_dim: int | None = None,
+                 layout: str = "kernel", stream=None) -> None:
+    """Bias add + NeoX RoPE + KV write in one launch (vaa_qkv_epilogue).
+
+    query [T, H, D], key/value [T, KV, D] (views into the planar QKV buffer
+    are fine: heads packed at stride D, key and value sharing strides), all
+    fp16 or all bf16 with the caches.  In place: q <- rope(q + b_q),
+    k <- rope(k + b_k), v <- v + b_v; K and V also go to their cache slot
+    (slot_mapping int32/int64, negative = padding).  bias: [H*D + 2*KV*D] in
+    the same type, or None.  Equals bias add, rope_neox_ and kv_write_slots
+    run in turn (engine/ops/qkv.py:391-416, elementwise.py:185-239,
+    kv_write.py:118-156).
+    """
+    _require_gpu(query, key, value, positions, cos_cache, sin_cache, slot_mapping, key_cache,
+                 value_cache, bias)
+    _attn_dtype(query=query, key=key, value=value, key_cache=key_cache,
+                value_cache=value_cache, bias=bias)
+    for t, n in ((query, "query"), (key, "key"), (value, "value")):
+        if t.dim() != 3 or t.stride(2) != 1 or t.stride(1) != t.shape[2]:
+            raise ValueError(f"{n} must be [tokens, heads, head_size] with heads packed")
+    if key.shape != value.shape or key.stride() != value.stride():
+        raise ValueError("key and value must have identical shapes and strides")
+    T, H, D = query.shape
+    if key.shape[0] != T or key.shape[2] != D:
+        raise ValueError("query/key token count or head_size differ")
+    if positions.dtype != torch.int32 or not positions.is_contiguous() or positions.numel() < T:
+        raise ValueError("positions must be a contiguous int32 tensor with one entry per token")
+    if slot_mapping.dtype not in (torch.int32, torch.int64) or not slot_mapping.is_contiguous() \
+            or slot_mapping.numel() < T:
+        raise ValueError("slot_mapping must be a contiguous int32/int64 tensor, one per token")
+    rot = rotary_dim or D
+    if cos_cache.dtype != torch.float32 or cos_cache.dim() != 2 or cos_cache.shape[1] != rot // 2 \
+            or sin_cache.shape != cos_cache.shape or not cos_cache.is_contiguous() \
+            or not sin_cache.is_contiguous():
+        raise ValueError("cos/sin caches must be contiguous fp32 [max_position, rotary_dim/2]")
+    KV = key.shape[1]
+    if bias is not None and (bias.dim() != 1 or bias.numel() != (H + 2 * KV) * D
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous [{(H + 2 * KV) * D}] vector")
+    p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
+                    num_query_heads=H, scale=1.0, query=query, new_kv=key)
+    if KV != p.num_kv_heads or D != p.head_size:
+        raise ValueError(f"key shape {tuple(key.shape)} does not match the cache")
+    itype = _lib.VAA_INDEX_I64 if slot_mapping.dtype == torch.int64 else _lib.VAA_INDEX_I32
+    _lib.call("vaa_qkv_epilogue", ctypes.byref(p), query.data_ptr(), key.data_ptr(),
+              value.data_ptr(), _ptr(bias), cos_cache.data_ptr(), sin_cache.data_ptr(), rot,
+              cos_cache.shape[0], positions.data_ptr(), slot_mapping.data_ptr(), itype,
+              key_cache.data_ptr(), value_cache.data_ptr(), T, _lib.stream_handle(stream))
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
              stream=None) -> torch.Tensor:
     """out = half(silu(float(gate)) * float(up)); 1-D or row-strided 2-D views."""
