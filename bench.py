@@ -46,7 +46,7 @@ def parse() -> argparse.Namespace:
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="headline",
-                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C2bf16", "all"],
+                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C2bf16", "topk", "all"],
                     help="headline = the contract line; the others print one JSON line per "
                          "BASELINE config (measurement record, not the driver's metric)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -361,8 +361,36 @@ def wl_c2bf16(args) -> dict:
     return _decode_record("C2-bf16", b, args, 0, "headline shape in bf16 (extension)")
 
 
+def wl_topk(args) -> dict:
+    """Top-k logits selection at the end of a step: k=50 (the reference's
+    default) over a 128256-entry vocabulary (the 32q/8kv hd128 family's), for
+    a decode batch of 32 rows and a 256-row batch.  torch.topk on the same
+    rows is timed beside it as a library reference point."""
+    import torch
+
+    from vllm_apple_amd import kernels
+
+    dev = torch.device("cuda:0")
+    V, k = 128256, 50
+    rec = {"workload": "topk", "note": f"vocab {V}, k={k}, fp16 logits resident in HBM"}
+    for T in (32, 256):
+        g = torch.Generator(device=dev).manual_seed(T)
+        logits = (torch.randn(T, V, generator=g, device=dev) * 4).half()
+        idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+        vals = torch.empty((T, k), dtype=torch.float16, device=dev)
+        t = _timed(lambda: kernels.topk_logits(logits, k, indices=idx, values=vals),
+                   args.steps, args.warmup)
+        t_torch = _timed(lambda: torch.topk(logits, k, dim=1), args.steps, args.warmup)
+        by = T * V * 2 + T * k * 6
+        rec[f"T{T}"] = {"ms": round(t, 5), "bytes": by,
+                        "gb_s": round(by / (t * 1e-3) / 1e9, 1),
+                        "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                        "torch_topk_ms": round(t_torch, 5)}
+    return rec
+
+
 WORKLOADS = {"C1": wl_c1, "C2u": wl_c2u, "C3": wl_c3, "C4": wl_c4, "C5": wl_c5,
-             "C2bf16": wl_c2bf16}
+             "C2bf16": wl_c2bf16, "topk": wl_topk}
 
 
 def main() -> int:
@@ -381,7 +409,7 @@ def main() -> int:
 
     _lib.load()
     if args.workload != "headline":
-        names = (["C1", "C2u", "C3", "C4", "C5", "C2bf16"] if args.workload == "all"
+        names = (["C1", "C2u", "C3", "C4", "C5", "C2bf16", "topk"] if args.workload == "all"
                  else [args.workload])
         for name in names:
             print(json.dumps(WORKLOADS[name](args)), flush=True)

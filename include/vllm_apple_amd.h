@@ -322,6 +322,34 @@ int vaa_qkv_epilogue(const vaa_attn_params* p, uint16_t* query, uint16_t* key,
                      int slot_index_type, uint16_t* key_cache, uint16_t* value_cache,
                      int num_tokens, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Top-k logits selection
+ * ---------------------------------------------------------------------- */
+
+/*
+ * The k largest values of each logits row and their column indices.
+ * Replaces topk_select / topk_select_small_k (vllm_apple/engine/ops/topk.py:40-412,
+ * host EngineTopK.encode :324-401), which cut the logits read back to the host
+ * to k entries per token.  logits: [num_tokens, vocab_size] 16-bit floats (fp16
+ * or bf16; the selection reads their bit patterns), 2-byte aligned, with
+ * row_stride elements between rows (16-byte aligned rows are read 16 bytes at a
+ * time).  Outputs indices int32 and values (the same 16-bit values)
+ * [num_tokens, k] with out_stride between rows, sorted by value descending,
+ * ties by lower column.  Values order as -NaN < -inf < ... < -0 < +0 < ... <
+ * +inf < +NaN.  1 <= k <= 256 and k <= vocab_size (the reference caps k at 50,
+ * or 8 on its small-k path); vocab_size <= 16384 * floor(4096 / k).
+ *
+ * A row is split over several workgroups when that fills the GPU better; the
+ * chunks' survivors then go through `workspace`, whose size
+ * vaa_topk_workspace_size returns (0: none needed, workspace may be null).  It
+ * depends only on (num_tokens, vocab_size, k).  VAA_ERR_WORKSPACE when it is
+ * missing, short or not 16-byte aligned.  Two launches at most, no allocation.
+ */
+int vaa_topk_workspace_size(int num_tokens, int vocab_size, int k, size_t* workspace_bytes);
+int vaa_topk_logits(const uint16_t* logits, int num_tokens, int vocab_size,
+                    int64_t row_stride, int k, int32_t* indices, uint16_t* values,
+                    int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -141,3 +141,51 @@ def test_dtype_and_epilogue_argument_errors(lib):
     # zero tokens is a no-op
     assert lib.vaa_qkv_epilogue(ctypes.byref(p), None, None, None, None, None, None, 128, 16,
                                 None, None, 0, None, None, 0, None) == 0
+
+
+def test_topk_argument_errors(lib):
+    """k outside 1..256 or above vocab_size, short strides, odd pointers and a
+    missing workspace are refused before any launch; zero tokens is a no-op."""
+    from vllm_apple_amd import _lib
+
+    fake = 0x10000  # never dereferenced: every call below fails its checks first
+    ws = ctypes.c_size_t(0)
+
+    def call(lg, T, V, rs, k, os_, w=None, wb=0):
+        return lib.vaa_topk_logits(lg, T, V, rs, k, fake, fake, os_, w, wb, None)
+
+    st = call(fake, 4, 1000, 1000, 257, 257)
+    assert st == _lib.VAA_ERR_UNSUPPORTED and "k=257" in _lib.last_error()
+    assert call(fake, 4, 10, 10, 11, 11) == _lib.VAA_ERR_UNSUPPORTED
+    st = call(fake, 4, 1000, 999, 8, 8)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "row_stride" in _lib.last_error()
+    assert call(fake, 4, 1000, 1000, 8, 7) == _lib.VAA_ERR_INVALID_ARG
+    st = call(fake + 1, 4, 1000, 1000, 8, 8)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "2-byte aligned" in _lib.last_error()
+    st = call(None, 4, 1000, 1000, 8, 8)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "null pointer" in _lib.last_error()
+    assert call(None, 0, 1000, 1000, 8, 8) == 0
+    # A vocabulary beyond what one merge holds for this k.
+    st = lib.vaa_topk_workspace_size(4, 16384 * 16 + 1, 256, ctypes.byref(ws))
+    assert st == _lib.VAA_ERR_UNSUPPORTED and "too large" in _lib.last_error()
+    # A split row needs the workspace; a short one is refused.
+    assert lib.vaa_topk_workspace_size(32, 128256, 50, ctypes.byref(ws)) == 0
+    assert ws.value > 0 and ws.value % (32 * 50 * 8) == 0
+    st = call(fake, 32, 128256, 128256, 50, 50)
+    assert st == _lib.VAA_ERR_WORKSPACE and "workspace" in _lib.last_error()
+    assert call(fake, 32, 128256, 128256, 50, 50, fake, ws.value - 8) == _lib.VAA_ERR_WORKSPACE
+
+
+def test_topk_workspace_size(lib):
+    """No workspace when a row is one chunk (<= 4096 columns) and the batch
+    alone fills the GPU; otherwise T * S * k * 8 bytes, S chunks of <= 16384
+    columns whose S * k survivors fit the merge (<= 4096)."""
+    ws = ctypes.c_size_t(0)
+    assert lib.vaa_topk_workspace_size(4096, 4096, 50, ctypes.byref(ws)) == 0
+    assert ws.value == 0
+    assert lib.vaa_topk_workspace_size(3, 8, 8, ctypes.byref(ws)) == 0 and ws.value == 0
+    for T, V, k in ((32, 128256, 50), (256, 151936, 256), (1, 262144, 256), (9, 32000, 1)):
+        assert lib.vaa_topk_workspace_size(T, V, k, ctypes.byref(ws)) == 0
+        S = ws.value // (T * k * 8)
+        assert ws.value == T * S * k * 8 and S >= 2
+        assert S * k <= 4096 and -(-V // S) <= 16384

@@ -30,6 +30,7 @@ SOURCES = [
     "layer_ops.hip",
     "index_ops.hip",
     "qkv_epilogue.hip",
+    "topk.hip",
 ]
 
 ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")

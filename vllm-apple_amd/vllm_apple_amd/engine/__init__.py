@@ -1,4 +1,4 @@
-"""Encode-only ops mirroring vllm_apple/engine/ops/{attention,kv_write,rmsnorm,elementwise}.py.
+"""Encode-only ops mirroring vllm_apple/engine/ops/{attention,kv_write,rmsnorm,elementwise,topk}.py.
 
 "Encode" here means: enqueue the HIP kernels on a stream and return without
 waiting.  Every encode_* method keeps the reference's argument names and order;
@@ -12,16 +12,19 @@ from .elementwise import EngineElementwiseOps, EngineRoPE
 from .kv_write import KVWriteOp, KVWriteParams
 from .rmsnorm import EngineRMSNorm, RMSNormConfig
 from .step import EngineStepContext
+from .topk import EngineTopK, reconstruct_logits
 
 __all__ = [
     "EngineElementwiseOps",
     "EngineRMSNorm",
     "EngineRoPE",
     "EngineStepContext",
+    "EngineTopK",
     "FusedAttentionParams",
     "KVWriteOp",
     "KVWriteParams",
     "PagedAttentionOp",
     "PagedAttentionParams",
     "RMSNormConfig",
+    "reconstruct_logits",
 ]

@@ -550,6 +550,59 @@ def qkv_epilogue(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
               key_cache.data_ptr(), value_cache.data_ptr(), T, _lib.stream_handle(stream))
 
 
+TOPK_MAX_K = 256
+
+
+_topk_workspaces: dict[int, torch.Tensor] = {}
+
+
+def topk_workspace_size(num_tokens: int, vocab_size: int, k: int) -> int:
+    """Bytes of workspace vaa_topk_logits needs (0 when a row fits one workgroup)."""
+    n = ctypes.c_size_t(0)
+    _lib.call("vaa_topk_workspace_size", num_tokens, vocab_size, k, ctypes.byref(n))
+    return int(n.value)
+
+
+def topk_logits(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = None,
+                values: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                stream=None) -> tuple:
+    """(indices int32 [T, k], values [T, k]): the k largest logits of each row,
+    value-descending, ties by lower column (vaa_topk_logits; the reference's
+    EngineTopK, engine/ops/topk.py:40-412).  logits: [T, V] fp16 or bf16 with
+    a contiguous last dim.  Without `workspace` a grow-only per-device buffer
+    is used, safe for calls ordered on one stream."""
+    _require_gpu(logits, indices, values, workspace)
+    if logits.dtype not in ATTN_DTYPES:
+        raise ValueError(f"logits must be float16 or bfloat16, got {logits.dtype}")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [tokens, vocab] with a contiguous last dim")
+    T, V = logits.shape
+    if not 1 <= k <= min(TOPK_MAX_K, V):
+        raise ValueError(f"k={k} must be in 1..{min(TOPK_MAX_K, V)}")
+    if indices is None:
+        indices = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    if values is None:
+        values = torch.empty((T, k), dtype=logits.dtype, device=logits.device)
+    if indices.dtype != torch.int32 or indices.shape != (T, k) or values.shape != (T, k) \
+            or values.dtype != logits.dtype or indices.stride() != values.stride() \
+            or indices.stride(1) != 1:
+        raise ValueError("indices/values must be [T, k] (int32 / the logits' type), same strides")
+    nbytes = topk_workspace_size(T, V, k)
+    if workspace is None and nbytes > 0:
+        idx = _dev_index(logits.device)
+        workspace = _topk_workspaces.get(idx)
+        if workspace is None or workspace.numel() < nbytes:
+            workspace = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8,
+                                    device=logits.device)
+            _topk_workspaces[idx] = workspace
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _lib.call("vaa_topk_logits", logits.data_ptr(), T, V, logits.stride(0), k,
+              indices.data_ptr(), values.data_ptr(), indices.stride(0), ws_ptr, ws_bytes,
+              _lib.stream_handle(stream))
+    return indices, values
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
              stream=None) -> torch.Tensor:
     """out = half(silu(float(gate)) * float(up)); 1-D or row-strided 2-D views."""
