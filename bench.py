@@ -328,6 +328,21 @@ def wl_c5(args) -> dict:
     n_qkv = qkv.numel() * 2
     epi_bytes = 2 * n_qkv + bias.numel() * 2 + T_ * (D_ // 2) * 4 * 2 + T_ * 8 \
         + 2 * T_ * KV_ * D_ * 2
+    # Residual add + RMSNorm: fused against the reference's residual add, copy
+    # into the residual buffer and norm (three passes, 7 row-sized accesses).
+    res_a = torch.randn(x.shape, generator=gq, device=dev).half()
+    res_b = res_a.clone()
+    h_buf = torch.empty_like(x)
+    t_addnorm = _timed(lambda: kernels.add_rms_norm(x, res_a, w, b.extra["eps"], out=y),
+                       args.steps, args.warmup)
+
+    def addnorm_three():
+        torch.add(x, res_b, out=h_buf)
+        res_b.copy_(h_buf)
+        kernels.rms_norm(h_buf, w, b.extra["eps"], out=h_buf)
+
+    t_addnorm3 = _timed(addnorm_three, args.steps, args.warmup)
+    addnorm_bytes = 4 * x.numel() * 2 + w.numel() * 2
     g, u = b.extra["gate"], b.extra["up"]
     act = torch.empty_like(g)
     t_silu = _timed(lambda: kernels.silu_mul(g, u, out=act), args.steps, args.warmup)
@@ -342,8 +357,10 @@ def wl_c5(args) -> dict:
            "attention_decode_kv_bytes": kv_read,
            "attention_prefill_flops": 4.0 * D * H * pre_ctx}
     rec["qkv_epilogue_three_pass_ms"] = round(t_three, 5)
+    rec["add_rmsnorm_three_pass_ms"] = round(t_addnorm3, 5)
     for nm, t, by in (("rmsnorm", t_norm, norm_bytes), ("rope", t_rope, rope_bytes),
-                      ("silu_mul", t_silu, silu_bytes), ("qkv_epilogue", t_epi, epi_bytes)):
+                      ("silu_mul", t_silu, silu_bytes), ("qkv_epilogue", t_epi, epi_bytes),
+                      ("add_rmsnorm", t_addnorm, addnorm_bytes)):
         rec[nm] = {"ms": round(t, 5), "bytes": by, "gb_s": round(by / (t * 1e-3) / 1e9, 1),
                    "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
     return rec

@@ -258,6 +258,20 @@ int vaa_rmsnorm(const uint16_t* input, uint16_t* output, const uint16_t* weight,
                 int64_t residual_stride, float eps, void* stream);
 
 /*
+ * Residual add + RMSNorm in one pass.  Replaces the reference layer's three
+ * steps between the O projection and the MLP, and between the MLP and the
+ * next layer's input norm (vllm_apple/engine/runner.py:871-887,1107-1130,
+ * 1165-1171: encode_residual_add, encode_copy into the residual buffer,
+ * EngineRMSNorm.encode in place):
+ *   h = half(float(input) + float(residual));  residual <- h;
+ *   output = half(float(h) * rsqrt(mean(float(h)^2) + eps) * float(w))
+ * bit for bit as those steps.  output may alias input, not residual.  fp16.
+ */
+int vaa_add_rmsnorm(const uint16_t* input, uint16_t* residual, const uint16_t* weight,
+                    uint16_t* output, int num_tokens, int hidden_size, int64_t input_stride,
+                    int64_t residual_stride, int64_t output_stride, float eps, void* stream);
+
+/*
  * NeoX (split-half) rotary embedding, in place on query [T, num_heads, D] and
  * key [T, num_kv_heads, D] (token strides given, heads contiguous at stride
  * head_size).  Replaces rope_neox_kernel (vllm_apple/engine/ops/elementwise.py:185-239,

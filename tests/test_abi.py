@@ -189,3 +189,18 @@ def test_topk_workspace_size(lib):
         S = ws.value // (T * k * 8)
         assert ws.value == T * S * k * 8 and S >= 2
         assert S * k <= 4096 and -(-V // S) <= 16384
+
+
+def test_add_rmsnorm_argument_errors(lib):
+    """Output over the residual, short strides and null pointers are refused
+    before any launch; zero tokens is a no-op."""
+    from vllm_apple_amd import _lib
+
+    a, b = 0x10000, 0x20000  # never dereferenced
+    st = lib.vaa_add_rmsnorm(a, b, a, b, 4, 128, 128, 128, 128, 1e-6, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "alias" in _lib.last_error()
+    st = lib.vaa_add_rmsnorm(a, b, a, a, 4, 128, 128, 64, 128, 1e-6, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "stride" in _lib.last_error()
+    st = lib.vaa_add_rmsnorm(a, None, a, a, 4, 128, 128, 128, 128, 1e-6, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "null" in _lib.last_error()
+    assert lib.vaa_add_rmsnorm(None, None, None, None, 0, 128, 128, 128, 128, 1e-6, None) == 0

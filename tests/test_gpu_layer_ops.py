@@ -27,6 +27,60 @@ def test_rmsnorm(gpu, T, H, residual):
     assert_close(host(out), ref, what=f"rmsnorm {T}x{H}")
 
 
+@pytest.mark.parametrize("T,H", [(37, 5120), (4, 896), (2104, 4096), (5, 20480), (9, 100)])
+def test_add_rmsnorm_equals_three_steps(gpu, T, H):
+    """vaa_add_rmsnorm against the reference layer's residual add, copy and
+    norm in place (runner.py:1107-1130), here torch's fp16 add, a copy and
+    vaa_rmsnorm: residual and output equal bit for bit.  Covers the register
+    path, the long-row two-pass path (H=20480) and the scalar path (H=100),
+    and the output written over x."""
+    from vllm_apple_amd import kernels
+
+    print(f"[case] add_rmsnorm T={T} H={H}", flush=True)
+    g = torch.Generator().manual_seed(T + H)
+    x = torch.randn(T, H, generator=g).half().cuda()
+    r = torch.randn(T, H, generator=g).half().cuda()
+    w = (torch.randn(H, generator=g) * 0.1 + 1).half().cuda()
+    h = x + r  # the reference's residual_add (half add)
+    res2 = h.clone()  # encode_copy into the residual buffer
+    out2 = kernels.rms_norm(h, w, 1e-6)  # EngineRMSNorm.encode
+    x1, r1 = x.clone(), r.clone()
+    kernels.add_rms_norm(x1, r1, w, 1e-6, out=x1)
+    torch.cuda.synchronize()
+    assert torch.equal(r1.view(torch.int16), res2.view(torch.int16)), "residual"
+    assert torch.equal(x1.view(torch.int16), out2.view(torch.int16)), "normed output"
+
+
+def test_add_rmsnorm_against_oracle_and_engine(gpu):
+    from vllm_apple_amd import kernels
+    from vllm_apple_amd.engine import EngineRMSNorm, EngineStepContext
+
+    T, H = 50, 2048
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(T, H, generator=g).half()
+    r = torch.randn(T, H, generator=g).half()
+    w = (torch.randn(H, generator=g) * 0.1 + 1).half()
+    h_ref = (host(x) + host(r)).astype(np.float16)  # one rounding, as a half add
+    ref = olo.rms_norm(h_ref, host(w), 1e-5)
+    rd = r.cuda()
+    out = kernels.add_rms_norm(x.cuda(), rd, w.cuda(), 1e-5)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(rd).view(np.uint16), h_ref.view(np.uint16)), "residual"
+    assert_close(host(out), ref, what="add_rmsnorm")
+    # Engine op on (buffer, byte offset) views inside an ENCODE phase.
+    buf = torch.zeros(3 * T * H + 64, dtype=torch.float16, device="cuda")
+    buf[64:64 + T * H] = x.cuda().reshape(-1)
+    buf[64 + T * H:64 + 2 * T * H] = r.cuda().reshape(-1)
+    norm = EngineRMSNorm(None, H, eps=1e-5, weight_buffer=w.cuda())
+    with EngineStepContext() as ctx:
+        norm.encode_residual_add_norm(ctx, (buf, 128), (buf, 128 + 2 * T * H), (buf, 128), T)
+    torch.cuda.synchronize()
+    assert torch.equal(buf[64:64 + T * H].view(T, H).cpu().view(torch.int16),
+                       out.cpu().view(torch.int16))
+    assert np.array_equal(host(buf[64 + T * H:64 + 2 * T * H].view(T, H)).view(np.uint16),
+                          h_ref.view(np.uint16))
+
+
 def test_rmsnorm_reference_known_case(gpu):
     """tests/metal/test_transformer_block.py:136-199 (seed 42, [4,128], eps 1e-6)."""
     from vllm_apple_amd import kernels

@@ -24,11 +24,17 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 // plus float(residual) after the norm when a residual is given.
 // One wave per row; NC 16-byte chunks per lane stay in registers so x is read
 // from HBM once (NC == 0: rows too long for registers, second pass re-reads).
+//
+// kAdd: the residual add that precedes the norm in the reference's layer
+// (runner.py:1107-1130: residual_add, copy to the residual buffer, norm in
+// place) in one pass: h = half(x + r) is written back to r, and the norm of h
+// goes to out (which may alias x).  The norm's arithmetic is the plain
+// kernel's on h, so the result equals the three steps bit for bit.
 constexpr int kNormRowsPerBlock = 4;
 
-template <int NC>
+template <int NC, bool kAdd>
 __global__ void __launch_bounds__(kNormRowsPerBlock* kWave)
-rmsnorm_vec_kernel(const f16* in, f16* out, const f16* w, const f16* res, int T,
+rmsnorm_vec_kernel(const f16* in, f16* out, const f16* w, f16* res, int T,
                    int H, int64_t in_st, int64_t out_st, int64_t res_st,
                    float eps) {
   const int row = blockIdx.x * kNormRowsPerBlock + threadIdx.x / kWave;
@@ -36,13 +42,30 @@ rmsnorm_vec_kernel(const f16* in, f16* out, const f16* w, const f16* res, int T,
   if (row >= T) return;
   const int chunks = H / 8;
   const f16* x = in + row * in_st;
+  f16* r = res ? res + row * res_st : nullptr;
+  // The row's values: x, or (kAdd) h = half(x + r), written back to r.
+  auto load = [&](int c) {
+    const u32x4 v = ld16(x + 8 * c);
+    if constexpr (!kAdd) {
+      return v;
+    } else {
+      float f[8], rf[8];
+      unpack8(v, f);
+      unpack8(ld16(r + 8 * c), rf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] += rf[e];
+      const u32x4 h = pack8(f);
+      st16(r + 8 * c, h);
+      return h;
+    }
+  };
   float ss = 0.f;
   u32x4 xv[NC > 0 ? NC : 1];
   if constexpr (NC > 0) {
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int c = lane + i * kWave;
-      xv[i] = c < chunks ? ld16(x + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+      xv[i] = c < chunks ? load(c) : u32x4{0u, 0u, 0u, 0u};
       float f[8];
       unpack8(xv[i], f);
 #pragma unroll
@@ -51,7 +74,7 @@ rmsnorm_vec_kernel(const f16* in, f16* out, const f16* w, const f16* res, int T,
   } else {
     for (int c = lane; c < chunks; c += kWave) {
       float f[8];
-      unpack8(ld16(x + 8 * c), f);
+      unpack8(load(c), f);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
     }
@@ -59,14 +82,13 @@ rmsnorm_vec_kernel(const f16* in, f16* out, const f16* w, const f16* res, int T,
   ss = wave_sum(ss);
   const float rs = rsqrtf(ss / static_cast<float>(H) + eps);
   f16* o = out + row * out_st;
-  const f16* r = res ? res + row * res_st : nullptr;
   auto emit = [&](int c, u32x4 v) {
     float f[8], wf[8];
     unpack8(v, f);
     unpack8(ld16(w + 8 * c), wf);
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = (f[e] * rs) * wf[e];
-    if (r) {
+    if (!kAdd && r) {
       float rf[8];
       unpack8(ld16(r + 8 * c), rf);
 #pragma unroll
@@ -81,29 +103,38 @@ rmsnorm_vec_kernel(const f16* in, f16* out, const f16* w, const f16* res, int T,
       if (c < chunks) emit(c, xv[i]);
     }
   } else {
-    for (int c = lane; c < chunks; c += kWave) emit(c, ld16(x + 8 * c));
+    // Second pass: h was written to r by this lane (kAdd), x otherwise.
+    for (int c = lane; c < chunks; c += kWave) emit(c, ld16((kAdd ? r : x) + 8 * c));
   }
 }
 
+template <bool kAdd>
 __global__ void __launch_bounds__(kNormRowsPerBlock* kWave)
-rmsnorm_scalar_kernel(const f16* in, f16* out, const f16* w, const f16* res,
+rmsnorm_scalar_kernel(const f16* in, f16* out, const f16* w, f16* res,
                       int T, int H, int64_t in_st, int64_t out_st,
                       int64_t res_st, float eps) {
   const int row = blockIdx.x * kNormRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= T) return;
   const f16* x = in + row * in_st;
+  f16* r = res ? res + row * res_st : nullptr;
   float ss = 0.f;
   for (int i = lane; i < H; i += kWave) {
-    const float v = h2f(x[i]);
+    float v = h2f(x[i]);
+    if constexpr (kAdd) {
+      const f16 h = f2h(v + h2f(r[i]));
+      r[i] = h;
+      v = h2f(h);
+    }
     ss += v * v;
   }
   ss = wave_sum(ss);
   const float rs = rsqrtf(ss / static_cast<float>(H) + eps);
   f16* o = out + row * out_st;
+  const f16* src = kAdd ? r : x;
   for (int i = lane; i < H; i += kWave) {
-    float v = (h2f(x[i]) * rs) * h2f(w[i]);
-    if (res) v += h2f(res[row * res_st + i]);
+    float v = (h2f(src[i]) * rs) * h2f(w[i]);
+    if (!kAdd && r) v += h2f(r[i]);
     o[i] = f2h(v);
   }
 }
@@ -230,6 +261,40 @@ int64_t grid_for(int64_t work, int64_t per_block, int64_t cap) {
 
 using namespace vaa;
 
+namespace vaa {
+namespace {
+
+template <bool kAdd>
+int launch_rmsnorm(const char* what, const f16* in, f16* out, const f16* w, f16* r, int T, int H,
+                   int64_t in_st, int64_t out_st, int64_t r_st, float eps, hipStream_t s) {
+  const dim3 grid((T + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
+  const dim3 block(kNormRowsPerBlock * kWave);
+  const bool vec = H % 8 == 0 && aligned16(in) && aligned16(out) && aligned16(w) &&
+                   (!r || aligned16(r)) && in_st % 8 == 0 && out_st % 8 == 0 &&
+                   (!r || r_st % 8 == 0);
+  if (!vec) {
+    hipLaunchKernelGGL(rmsnorm_scalar_kernel<kAdd>, grid, block, 0, s, in, out, w, r, T, H,
+                       in_st, out_st, r_st, eps);
+    return check_launch(what);
+  }
+  const int per_lane = (H / 8 + kWave - 1) / kWave;
+#define VAA_NORM(NC)                                                                       \
+  hipLaunchKernelGGL((rmsnorm_vec_kernel<NC, kAdd>), grid, block, 0, s, in, out, w, r, T, H, \
+                     in_st, out_st, r_st, eps)
+  if (per_lane <= 1) VAA_NORM(1);
+  else if (per_lane <= 2) VAA_NORM(2);
+  else if (per_lane <= 4) VAA_NORM(4);
+  else if (per_lane <= 8) VAA_NORM(8);
+  else if (per_lane <= 10) VAA_NORM(10);
+  else if (per_lane <= 16) VAA_NORM(16);
+  else VAA_NORM(0);
+#undef VAA_NORM
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace vaa
+
 extern "C" int vaa_rmsnorm(const uint16_t* input, uint16_t* output,
                            const uint16_t* weight, const uint16_t* residual,
                            int num_tokens, int hidden_size, int64_t input_stride,
@@ -244,36 +309,35 @@ extern "C" int vaa_rmsnorm(const uint16_t* input, uint16_t* output,
   if (input_stride < hidden_size || output_stride < hidden_size ||
       (residual && residual_stride < hidden_size))
     return fail(VAA_ERR_INVALID_ARG, "vaa_rmsnorm: row stride < hidden_size");
-  const f16* in = reinterpret_cast<const f16*>(input);
-  f16* out = reinterpret_cast<f16*>(output);
-  const f16* w = reinterpret_cast<const f16*>(weight);
-  const f16* r = reinterpret_cast<const f16*>(residual);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((num_tokens + kNormRowsPerBlock - 1) / kNormRowsPerBlock);
-  const dim3 block(kNormRowsPerBlock * kWave);
-  const bool vec = hidden_size % 8 == 0 && aligned16(in) && aligned16(out) &&
-                   aligned16(w) && (!r || aligned16(r)) && input_stride % 8 == 0 &&
-                   output_stride % 8 == 0 && (!r || residual_stride % 8 == 0);
-  if (!vec) {
-    hipLaunchKernelGGL(rmsnorm_scalar_kernel, grid, block, 0, s, in, out, w, r,
-                       num_tokens, hidden_size, input_stride, output_stride,
-                       residual_stride, eps);
-    return check_launch("rmsnorm_scalar_kernel");
-  }
-  const int per_lane = (hidden_size / 8 + kWave - 1) / kWave;
-#define VAA_NORM(NC)                                                            \
-  hipLaunchKernelGGL(rmsnorm_vec_kernel<NC>, grid, block, 0, s, in, out, w, r,  \
-                     num_tokens, hidden_size, input_stride, output_stride,      \
-                     residual_stride, eps)
-  if (per_lane <= 1) VAA_NORM(1);
-  else if (per_lane <= 2) VAA_NORM(2);
-  else if (per_lane <= 4) VAA_NORM(4);
-  else if (per_lane <= 8) VAA_NORM(8);
-  else if (per_lane <= 10) VAA_NORM(10);
-  else if (per_lane <= 16) VAA_NORM(16);
-  else VAA_NORM(0);
-#undef VAA_NORM
-  return check_launch("rmsnorm_vec_kernel");
+  // The residual is only read here.
+  return launch_rmsnorm<false>(
+      "rmsnorm_kernel", reinterpret_cast<const f16*>(input), reinterpret_cast<f16*>(output),
+      reinterpret_cast<const f16*>(weight),
+      const_cast<f16*>(reinterpret_cast<const f16*>(residual)), num_tokens, hidden_size,
+      input_stride, output_stride, residual_stride, eps, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int vaa_add_rmsnorm(const uint16_t* input, uint16_t* residual, const uint16_t* weight,
+                               uint16_t* output, int num_tokens, int hidden_size,
+                               int64_t input_stride, int64_t residual_stride,
+                               int64_t output_stride, float eps, void* stream) {
+  const char* what = "vaa_add_rmsnorm";
+  if (num_tokens < 0 || hidden_size <= 0)
+    return fail(VAA_ERR_INVALID_ARG, "%s: num_tokens=%d hidden_size=%d", what, num_tokens,
+                hidden_size);
+  if (num_tokens == 0) return VAA_OK;
+  if (!input || !residual || !weight || !output)
+    return fail(VAA_ERR_INVALID_ARG, "%s: null pointer", what);
+  if (input_stride < hidden_size || output_stride < hidden_size ||
+      residual_stride < hidden_size)
+    return fail(VAA_ERR_INVALID_ARG, "%s: row stride < hidden_size", what);
+  if (static_cast<const void*>(output) == static_cast<const void*>(residual))
+    return fail(VAA_ERR_INVALID_ARG, "%s: output must not alias residual", what);
+  return launch_rmsnorm<true>(
+      "add_rmsnorm_kernel", reinterpret_cast<const f16*>(input), reinterpret_cast<f16*>(output),
+      reinterpret_cast<const f16*>(weight), reinterpret_cast<f16*>(residual), num_tokens,
+      hidden_size, input_stride, output_stride, residual_stride, eps,
+      static_cast<hipStream_t>(stream));
 }
 
 extern "C" int vaa_rope_neox(uint16_t* query, uint16_t* key,

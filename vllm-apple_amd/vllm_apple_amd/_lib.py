@@ -96,6 +96,7 @@ SIGNATURES = {
     "vaa_build_token_index": (_I, [_P, _P, _I, _I, _P, _P, _P]),
     "vaa_build_slot_mapping": (_I, [_P, _I, _I, _P, _P, _I, _I, _P, _P]),
     "vaa_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _F, _P]),
+    "vaa_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _F, _P]),
     "vaa_rope_neox": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64, _I, _P]),
     "vaa_silu_mul": (_I, [_P, _P, _P, _I64, _P]),
     "vaa_silu_mul_2d": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),

@@ -453,6 +453,31 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *,
     return out
 
 
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float, *,
+                 out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """residual <- half(x + residual); out = rms_norm(residual) (vaa_add_rmsnorm).
+    One pass for the reference layer's residual add, copy and norm
+    (runner.py:1107-1130).  out may be x itself (the reference's in-place
+    hidden buffer) but not residual."""
+    _require_gpu(x, residual, weight, out)
+    for t, n in ((x, "x"), (residual, "residual"), (weight, "weight")):
+        _require_dtype(t, torch.float16, n)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be [num_tokens, hidden] with contiguous rows")
+    t, h = x.shape
+    if weight.numel() != h or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [hidden] tensor")
+    if out is None:
+        out = torch.empty_like(x)
+    for r, n in ((out, "out"), (residual, "residual")):
+        if r.shape != x.shape or r.stride(1) != 1 or r.dtype != torch.float16:
+            raise ValueError(f"{n} must match x ([T, H] fp16, contiguous rows)")
+    _lib.call("vaa_add_rmsnorm", x.data_ptr(), residual.data_ptr(), weight.data_ptr(),
+              out.data_ptr(), t, h, x.stride(0), residual.stride(0), out.stride(0), float(eps),
+              _lib.stream_handle(stream))
+    return out
+
+
 def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float,
                        device: torch.device | str = "cuda") -> tuple[torch.Tensor, torch.Tensor]:
     """fp32 cos/sin tables [max_position, rotary_dim // 2].
