@@ -177,6 +177,24 @@ def _timed(fn, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def _timed_rot(fns, steps: int, warmup: int) -> float:
+    """_timed over a rotation: call i runs fns[i % len(fns)], each on its own
+    copy of the data, so the bytes touched per rotation exceed the 256 MB
+    Infinity Cache and a bandwidth figure is not inflated by cache hits."""
+    state = {"i": 0}
+
+    def call():
+        fns[state["i"] % len(fns)]()
+        state["i"] += 1
+
+    return _timed(call, steps, warmup)
+
+
+def _copies(nbytes: int, floor: int = 1) -> int:
+    """Copies of a working set of nbytes needed to touch more than 256 MB."""
+    return max(floor, -(-300_000_000 // max(1, nbytes)))
+
+
 def _decode_record(name: str, b, args, partition: int, note: str) -> dict:
     import torch
 
@@ -252,8 +270,14 @@ def wl_c3(args) -> dict:
 
     b = workloads.c3_prefill(device=torch.device("cuda:0"))
     out = torch.empty_like(b.query)
-    t_kv = _timed(lambda: kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache,
-                                                 b.slot_mapping), args.steps, args.warmup)
+    # KV write: each rotation copy has its own new K/V and its own cache.
+    T = b.query.shape[0]
+    kv_bytes = 2 * 2 * T * b.num_kv_heads * b.head_size * 2 + T * 8
+    kv_sets = [(b.new_k.clone(), b.new_v.clone(), b.k_cache.clone(), b.v_cache.clone())
+               for _ in range(_copies(kv_bytes))]
+    t_kv = _timed_rot([lambda s=s_: kernels.kv_write_slots(s[0], s[1], s[2], s[3], b.slot_mapping)
+                       for s_ in kv_sets], args.steps, args.warmup)
+    del kv_sets
     t_at = _timed(lambda: kernels.paged_prefill(b.query, b.k_cache, b.v_cache, b.block_table,
                                                 b.token_to_seq, b.positions, scale=b.scale,
                                                 output=out), args.steps, args.warmup)
@@ -263,8 +287,6 @@ def wl_c3(args) -> dict:
     t_bf = _timed(lambda: kernels.paged_prefill(bb.query, bb.k_cache, bb.v_cache, bb.block_table,
                                                 bb.token_to_seq, bb.positions, scale=bb.scale,
                                                 output=out_b), args.steps, args.warmup)
-    T = b.query.shape[0]
-    kv_bytes = 2 * 2 * T * b.num_kv_heads * b.head_size * 2 + T * 8
     return {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
             "tokens": T, "kv_write_ms": round(t_kv, 5),
             "kv_write_gb_s": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
@@ -297,51 +319,72 @@ def wl_c5(args) -> dict:
                               output=out[nd:])
 
     t_attn = _timed(attn_step, args.steps, args.warmup)
+    # Layer ops: each timed over a rotation of input/output copies whose bytes
+    # exceed the 256 MB Infinity Cache.
     x, w = b.extra["hidden"], b.extra["norm_weight"]
     y = torch.empty_like(x)
-    t_norm = _timed(lambda: kernels.rms_norm(x, w, b.extra["eps"], out=y), args.steps, args.warmup)
+    eps = b.extra["eps"]
+    norm_sets = [(x.clone(), torch.empty_like(x)) for _ in range(_copies(2 * x.numel() * 2))]
+    t_norm = _timed_rot([lambda s=s_: kernels.rms_norm(s[0], w, eps, out=s[1])
+                         for s_ in norm_sets], args.steps, args.warmup)
+    del norm_sets
     cos, sin = kernels.rope_cos_sin_cache(b.head_size, 16384, b.extra["rope_base"], device=dev)
     q2, k2 = b.query.clone(), b.new_k.clone()
-    t_rope = _timed(lambda: kernels.rope_neox_(q2, k2, cos, sin, b.positions), args.steps,
-                    args.warmup)
+    rope_sets = [(q2.clone(), k2.clone())
+                 for _ in range(_copies((q2.numel() + k2.numel()) * 2))]
+    t_rope = _timed_rot([lambda s=s_: kernels.rope_neox_(s[0], s[1], cos, sin, b.positions)
+                         for s_ in rope_sets], args.steps, args.warmup)
+    del rope_sets
     # QKV epilogue over the step's planar QKV views: fused (one launch) against
     # the reference's three passes (bias add, RoPE, KV write).
     T_, H_, KV_, D_ = T, b.num_q_heads, b.num_kv_heads, b.head_size
     gq = torch.Generator(device=dev).manual_seed(7)
     qkv = torch.randn(T_ * (H_ + 2 * KV_) * D_, generator=gq, device=dev).half()
     bias = torch.randn((H_ + 2 * KV_) * D_, generator=gq, device=dev).half()
-    qv = qkv[:T_ * H_ * D_].view(T_, H_, D_)
-    kv_ = qkv[T_ * H_ * D_:T_ * (H_ + KV_) * D_].view(T_, KV_, D_)
-    vv = qkv[T_ * (H_ + KV_) * D_:].view(T_, KV_, D_)
-    t_epi = _timed(lambda: kernels.qkv_epilogue(qv, kv_, vv, b.positions, cos, sin,
-                                                b.slot_mapping, b.k_cache, b.v_cache,
-                                                bias=bias), args.steps, args.warmup)
+    def epi_views(buf):
+        return (buf[:T_ * H_ * D_].view(T_, H_, D_),
+                buf[T_ * H_ * D_:T_ * (H_ + KV_) * D_].view(T_, KV_, D_),
+                buf[T_ * (H_ + KV_) * D_:].view(T_, KV_, D_))
 
-    def three_step():
+    # Rotation: own QKV buffer and own (random, distinct) cache slots per copy.
+    n_slots = b.k_cache.shape[0] * b.k_cache.shape[2]
+    epi_sets = [(epi_views(qkv.clone()),
+                 torch.randperm(n_slots, generator=gq, device=dev)[:T_].to(torch.int64))
+                for _ in range(_copies(qkv.numel() * 2 * 2))]
+    t_epi = _timed_rot([lambda s=s_: kernels.qkv_epilogue(*s[0], b.positions, cos, sin, s[1],
+                                                          b.k_cache, b.v_cache, bias=bias)
+                        for s_ in epi_sets], args.steps, args.warmup)
+
+    def three_step(s):
+        (qv, kv_, vv), slots = s
         qv.add_(bias[:H_ * D_].view(1, H_, D_))
         kv_.add_(bias[H_ * D_:(H_ + KV_) * D_].view(1, KV_, D_))
         vv.add_(bias[(H_ + KV_) * D_:].view(1, KV_, D_))
         kernels.rope_neox_(qv, kv_, cos, sin, b.positions)
-        kernels.kv_write_slots(kv_, vv, b.k_cache, b.v_cache, b.slot_mapping)
+        kernels.kv_write_slots(kv_, vv, b.k_cache, b.v_cache, slots)
 
-    t_three = _timed(three_step, args.steps, args.warmup)
+    t_three = _timed_rot([lambda s=s_: three_step(s) for s_ in epi_sets], args.steps,
+                         args.warmup)
+    del epi_sets
     n_qkv = qkv.numel() * 2
     epi_bytes = 2 * n_qkv + bias.numel() * 2 + T_ * (D_ // 2) * 4 * 2 + T_ * 8 \
         + 2 * T_ * KV_ * D_ * 2
     # Residual add + RMSNorm: fused against the reference's residual add, copy
     # into the residual buffer and norm (three passes, 7 row-sized accesses).
     res_a = torch.randn(x.shape, generator=gq, device=dev).half()
-    res_b = res_a.clone()
-    h_buf = torch.empty_like(x)
-    t_addnorm = _timed(lambda: kernels.add_rms_norm(x, res_a, w, b.extra["eps"], out=y),
-                       args.steps, args.warmup)
+    an_sets = [(x.clone(), res_a.clone(), torch.empty_like(x))
+               for _ in range(_copies(3 * x.numel() * 2))]
+    t_addnorm = _timed_rot([lambda s=s_: kernels.add_rms_norm(s[0], s[1], w, eps, out=s[2])
+                            for s_ in an_sets], args.steps, args.warmup)
 
-    def addnorm_three():
-        torch.add(x, res_b, out=h_buf)
-        res_b.copy_(h_buf)
-        kernels.rms_norm(h_buf, w, b.extra["eps"], out=h_buf)
+    def addnorm_three(s):
+        torch.add(s[0], s[1], out=s[2])
+        s[1].copy_(s[2])
+        kernels.rms_norm(s[2], w, eps, out=s[2])
 
-    t_addnorm3 = _timed(addnorm_three, args.steps, args.warmup)
+    t_addnorm3 = _timed_rot([lambda s=s_: addnorm_three(s) for s_ in an_sets], args.steps,
+                            args.warmup)
+    del an_sets
     addnorm_bytes = 4 * x.numel() * 2 + w.numel() * 2
     g, u = b.extra["gate"], b.extra["up"]
     act = torch.empty_like(g)
@@ -395,8 +438,10 @@ def wl_topk(args) -> dict:
         logits = (torch.randn(T, V, generator=g, device=dev) * 4).half()
         idx = torch.empty((T, k), dtype=torch.int32, device=dev)
         vals = torch.empty((T, k), dtype=torch.float16, device=dev)
-        t = _timed(lambda: kernels.topk_logits(logits, k, indices=idx, values=vals),
-                   args.steps, args.warmup)
+        rows = [logits.clone() for _ in range(_copies(logits.numel() * 2))]
+        t = _timed_rot([lambda lg=lg_: kernels.topk_logits(lg, k, indices=idx, values=vals)
+                        for lg_ in rows], args.steps, args.warmup)
+        del rows
         t_torch = _timed(lambda: torch.topk(logits, k, dim=1), args.steps, args.warmup)
         by = T * V * 2 + T * k * 6
         rec[f"T{T}"] = {"ms": round(t, 5), "bytes": by,
