@@ -7,9 +7,10 @@
  * status code (VAA_OK == 0, negative on error); vaa_last_error() returns a
  * thread-local message for the last failure on the calling thread.
  *
- * Data types: K/V cache, queries, outputs and activations are IEEE fp16
- * (uint16_t storage); the attention entry points also take bfloat16 through
- * vaa_attn_params.dtype.  Block tables, sequence lengths, token->sequence maps
+ * Data types: K/V cache, queries, outputs and activations are 16-bit floats
+ * (uint16_t storage): IEEE fp16, the reference's type, or bfloat16, chosen by
+ * vaa_attn_params.dtype for the attention entry points and by a dtype
+ * argument (VAA_DTYPE_F16 / VAA_DTYPE_BF16) for the layer ops.  Block tables, sequence lengths, token->sequence maps
  * and positions are int32.  Slot mappings may be int32 (engine) or int64
  * (vLLM metadata), selected by an argument.
  *
@@ -37,7 +38,7 @@
 extern "C" {
 #endif
 
-#define VAA_ABI_VERSION 2
+#define VAA_ABI_VERSION 3
 
 enum {
   VAA_OK = 0,
@@ -242,7 +243,9 @@ int vaa_build_slot_mapping(const int32_t* block_table, int max_blocks_per_seq,
                            void* stream);
 
 /* ------------------------------------------------------------------------
- * Layer ops next to attention
+ * Layer ops next to attention.  `dtype` is VAA_DTYPE_F16 (the reference's
+ * fp16) or VAA_DTYPE_BF16 for every 16-bit tensor of the call; arithmetic is
+ * fp32, results round to nearest even.  Another value is VAA_ERR_UNSUPPORTED.
  * ---------------------------------------------------------------------- */
 
 /*
@@ -255,7 +258,7 @@ int vaa_build_slot_mapping(const int32_t* block_table, int max_blocks_per_seq,
 int vaa_rmsnorm(const uint16_t* input, uint16_t* output, const uint16_t* weight,
                 const uint16_t* residual, int num_tokens, int hidden_size,
                 int64_t input_stride, int64_t output_stride,
-                int64_t residual_stride, float eps, void* stream);
+                int64_t residual_stride, float eps, int dtype, void* stream);
 
 /*
  * Residual add + RMSNorm in one pass.  Replaces the reference layer's three
@@ -265,11 +268,12 @@ int vaa_rmsnorm(const uint16_t* input, uint16_t* output, const uint16_t* weight,
  * EngineRMSNorm.encode in place):
  *   h = half(float(input) + float(residual));  residual <- h;
  *   output = half(float(h) * rsqrt(mean(float(h)^2) + eps) * float(w))
- * bit for bit as those steps.  output may alias input, not residual.  fp16.
+ * bit for bit as those steps.  output may alias input, not residual.
  */
 int vaa_add_rmsnorm(const uint16_t* input, uint16_t* residual, const uint16_t* weight,
                     uint16_t* output, int num_tokens, int hidden_size, int64_t input_stride,
-                    int64_t residual_stride, int64_t output_stride, float eps, void* stream);
+                    int64_t residual_stride, int64_t output_stride, float eps, int dtype,
+                    void* stream);
 
 /*
  * NeoX (split-half) rotary embedding, in place on query [T, num_heads, D] and
@@ -283,15 +287,15 @@ int vaa_rope_neox(uint16_t* query, uint16_t* key, const float* cos_cache,
                   const float* sin_cache, const int32_t* positions,
                   int num_tokens, int num_heads, int num_kv_heads,
                   int head_size, int rotary_dim, int64_t q_stride_token,
-                  int64_t k_stride_token, int max_position, void* stream);
+                  int64_t k_stride_token, int max_position, int dtype, void* stream);
 
 /*
- * SwiGLU: out = half(silu(float(g)) * float(u)).  Replaces silu_mul_kernel
+ * SwiGLU: out = round16(silu(float(g)) * float(u)).  Replaces silu_mul_kernel
  * (vllm_apple/engine/ops/elementwise.py:114-124, host encode_silu_mul
  * :496-532) over num_elements contiguous elements.
  */
 int vaa_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* output,
-                 int64_t num_elements, void* stream);
+                 int64_t num_elements, int dtype, void* stream);
 
 /*
  * Row-strided SwiGLU over [rows, cols] (e.g. gate/up halves of vLLM's
@@ -300,7 +304,7 @@ int vaa_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* output,
  */
 int vaa_silu_mul_2d(const uint16_t* gate, const uint16_t* up, uint16_t* output,
                     int64_t rows, int64_t cols, int64_t gate_stride,
-                    int64_t up_stride, int64_t output_stride, void* stream);
+                    int64_t up_stride, int64_t output_stride, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused QKV epilogue

@@ -77,7 +77,7 @@ def test_params_struct_layout_matches_header(tmp_path):
 
 
 def test_version_and_error_string_without_gpu(lib):
-    assert lib.vaa_abi_version() == 2
+    assert lib.vaa_abi_version() == 3
     from vllm_apple_amd import _lib
 
     assert isinstance(_lib.last_error(), str)
@@ -95,7 +95,7 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
     assert "head_size=80" in _lib.last_error()
     with pytest.raises(NotImplementedError):
         _lib.check(st, "decode")
-    st = lib.vaa_rmsnorm(None, None, None, None, 4, 0, 0, 0, 0, 1e-5, None)
+    st = lib.vaa_rmsnorm(None, None, None, None, 4, 0, 0, 0, 0, 1e-5, 0, None)
     assert st == _lib.VAA_ERR_INVALID_ARG
     with pytest.raises(ValueError):
         _lib.check(st, "rmsnorm")
@@ -112,7 +112,7 @@ def test_zero_sized_calls_are_noops(lib):
     p = _lib.VaaAttnParams()
     p.num_kv_heads, p.head_size, p.block_size, p.num_blocks = 2, 64, 16, 4
     assert lib.vaa_kv_write_slots(ctypes.byref(p), None, None, None, 0, None, None, 0, None) == 0
-    assert lib.vaa_silu_mul(None, None, None, 0, None) == 0
+    assert lib.vaa_silu_mul(None, None, None, 0, 0, None) == 0
     assert lib.vaa_build_token_index(None, None, 0, 0, None, None, None) == 0
 
 
@@ -197,10 +197,26 @@ def test_add_rmsnorm_argument_errors(lib):
     from vllm_apple_amd import _lib
 
     a, b = 0x10000, 0x20000  # never dereferenced
-    st = lib.vaa_add_rmsnorm(a, b, a, b, 4, 128, 128, 128, 128, 1e-6, None)
+    st = lib.vaa_add_rmsnorm(a, b, a, b, 4, 128, 128, 128, 128, 1e-6, 0, None)
     assert st == _lib.VAA_ERR_INVALID_ARG and "alias" in _lib.last_error()
-    st = lib.vaa_add_rmsnorm(a, b, a, a, 4, 128, 128, 64, 128, 1e-6, None)
+    st = lib.vaa_add_rmsnorm(a, b, a, a, 4, 128, 128, 64, 128, 1e-6, 0, None)
     assert st == _lib.VAA_ERR_INVALID_ARG and "stride" in _lib.last_error()
-    st = lib.vaa_add_rmsnorm(a, None, a, a, 4, 128, 128, 128, 128, 1e-6, None)
+    st = lib.vaa_add_rmsnorm(a, None, a, a, 4, 128, 128, 128, 128, 1e-6, 0, None)
     assert st == _lib.VAA_ERR_INVALID_ARG and "null" in _lib.last_error()
-    assert lib.vaa_add_rmsnorm(None, None, None, None, 0, 128, 128, 128, 128, 1e-6, None) == 0
+    assert lib.vaa_add_rmsnorm(None, None, None, None, 0, 128, 128, 128, 128, 1e-6, 0, None) == 0
+
+
+def test_layer_op_dtype_errors(lib):
+    """A dtype outside {F16, BF16} is refused by every layer op before any launch."""
+    from vllm_apple_amd import _lib
+
+    a = 0x10000  # never dereferenced
+    assert lib.vaa_rmsnorm(a, a, a, None, 4, 128, 128, 128, 0, 1e-6, 5,
+                           None) == _lib.VAA_ERR_UNSUPPORTED
+    assert "dtype=5" in _lib.last_error()
+    assert lib.vaa_add_rmsnorm(a, a + 64, a, a, 4, 128, 128, 128, 128, 1e-6, 2,
+                               None) == _lib.VAA_ERR_UNSUPPORTED
+    assert lib.vaa_rope_neox(a, None, a, a, a, 4, 2, 0, 64, 64, 128, 0, 16, 9,
+                             None) == _lib.VAA_ERR_UNSUPPORTED
+    assert lib.vaa_silu_mul(a, a, a, 16, -1, None) == _lib.VAA_ERR_UNSUPPORTED
+    assert lib.vaa_silu_mul_2d(a, a, a, 2, 16, 16, 16, 16, 3, None) == _lib.VAA_ERR_UNSUPPORTED

@@ -43,13 +43,12 @@ def _views(buf, T, H, KV, D):
 
 @pytest.mark.parametrize("with_bias", [True, False])
 @pytest.mark.parametrize("rot", [128, 64])
-def test_epilogue_equals_three_step_path(gpu, with_bias, rot):
-    """fp16 (the RoPE kernel's type); bf16 is covered against the oracle below."""
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_epilogue_equals_three_step_path(gpu, with_bias, rot, dtype):
     from vllm_apple_amd import kernels
 
     T, H, KV, D, nb = 77, 32, 8, 128, 40
-    dtype = torch.float16
-    print(f"[case] epilogue vs 3-step bias={with_bias} rot={rot}", flush=True)
+    print(f"[case] epilogue vs 3-step bias={with_bias} rot={rot} {dtype}", flush=True)
     qkv, bias, kc, vc, slots, pos = _case(T, H, KV, D, nb, seed=1, dtype=dtype)
     pos[3] = 5000  # past the table: biased, not rotated
     cos, sin = kernels.rope_cos_sin_cache(rot, 4096, 1e6, device="cuda")

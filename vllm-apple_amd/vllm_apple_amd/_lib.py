@@ -34,7 +34,7 @@ VAA_PARTITION_BALANCED = -1
 # Element types of caches, queries, new K/V and outputs (vaa_attn_params.dtype).
 VAA_DTYPE_F16 = 0
 VAA_DTYPE_BF16 = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class NativeLibraryError(RuntimeError):
@@ -95,11 +95,11 @@ SIGNATURES = {
     "vaa_paged_attention_prefill": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "vaa_build_token_index": (_I, [_P, _P, _I, _I, _P, _P, _P]),
     "vaa_build_slot_mapping": (_I, [_P, _I, _I, _P, _P, _I, _I, _P, _P]),
-    "vaa_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _F, _P]),
-    "vaa_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _F, _P]),
-    "vaa_rope_neox": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64, _I, _P]),
-    "vaa_silu_mul": (_I, [_P, _P, _P, _I64, _P]),
-    "vaa_silu_mul_2d": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+    "vaa_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _F, _I, _P]),
+    "vaa_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _F, _I, _P]),
+    "vaa_rope_neox": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64, _I, _I, _P]),
+    "vaa_silu_mul": (_I, [_P, _P, _P, _I64, _I, _P]),
+    "vaa_silu_mul_2d": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P]),
     "vaa_topk_workspace_size": (_I, [_I, _I, _I, _P]),
     "vaa_topk_logits": (_I, [_P, _I, _I, _I64, _I, _P, _P, _I64, _P, ctypes.c_size_t, _P]),
     "vaa_qkv_epilogue": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _I,

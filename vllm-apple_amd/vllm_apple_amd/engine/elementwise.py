@@ -16,13 +16,15 @@ from .. import kernels
 from .step import resolve_stream, view
 
 
-def _as_view(x: Any, shape, dtype=torch.float16) -> torch.Tensor:
+def _as_view(x: Any, shape, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Typed view of a tensor or (tensor, byte offset); dtype None keeps the
+    buffer's own 16-bit type (fp16 or bf16)."""
     if isinstance(x, tuple):
         buf, off = x
-        return view(buf, off, shape, dtype)
+        return view(buf, off, shape, dtype or buf.dtype)
     if tuple(x.shape) == tuple(shape):
         return x
-    return view(x, 0, shape, dtype)
+    return view(x, 0, shape, dtype or x.dtype)
 
 
 class EngineElementwiseOps:

@@ -49,12 +49,12 @@ class EngineRMSNorm:
         H = self.config.hidden_size
         ib, io = self._buf(input_buffer)
         ob, oo = self._buf(output_buffer)
-        x = view(ib, io, (num_tokens, H))
-        out = view(ob, oo, (num_tokens, H))
+        x = view(ib, io, (num_tokens, H), dtype=ib.dtype)
+        out = view(ob, oo, (num_tokens, H), dtype=ob.dtype)
         res = None
         if residual_buffer is not None:
             rb, ro = self._buf(residual_buffer)
-            res = view(rb, ro, (num_tokens, H))
+            res = view(rb, ro, (num_tokens, H), dtype=rb.dtype)
         w = self._weight_buffer.reshape(-1)[:H]
         kernels.rms_norm(x, w, self.config.eps, residual=res, out=out, stream=stream)
 
@@ -70,9 +70,9 @@ class EngineRMSNorm:
         ib, io = self._buf(input_buffer)
         rb, ro = self._buf(residual_buffer)
         ob, oo = self._buf(output_buffer)
-        x = view(ib, io, (num_tokens, H))
-        res = view(rb, ro, (num_tokens, H))
-        out = view(ob, oo, (num_tokens, H))
+        x = view(ib, io, (num_tokens, H), dtype=ib.dtype)
+        res = view(rb, ro, (num_tokens, H), dtype=rb.dtype)
+        out = view(ob, oo, (num_tokens, H), dtype=ob.dtype)
         w = self._weight_buffer.reshape(-1)[:H]
         kernels.add_rms_norm(x, res, w, self.config.eps, out=out, stream=stream)
 

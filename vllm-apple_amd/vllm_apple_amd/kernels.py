@@ -430,13 +430,19 @@ def build_slot_mapping(block_table: torch.Tensor, block_size: int, token_to_seq:
 # ----------------------------------------------------------------- layer ops
 
 
+def _layer_dtype(**named: torch.Tensor | None) -> int:
+    """VAA_DTYPE_* code of a layer op's 16-bit tensors: all fp16 (the
+    reference's type) or all bf16."""
+    return ATTN_DTYPES[_attn_dtype(**named)]
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *,
              residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
              stream=None) -> torch.Tensor:
-    """half(x * rsqrt(mean(x^2) + eps) * w) [+ residual], rows of a 2-D view."""
+    """round16(x * rsqrt(mean(x^2) + eps) * w) [+ residual], rows of a 2-D view;
+    fp16 or bf16."""
     _require_gpu(x, weight, residual, out)
-    _require_dtype(x, torch.float16, "x")
-    _require_dtype(weight, torch.float16, "weight")
+    dt = _layer_dtype(x=x, weight=weight, residual=residual, out=out)
     if x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be [num_tokens, hidden] with contiguous rows")
     t, h = x.shape
@@ -445,11 +451,11 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *,
     if out is None:
         out = torch.empty_like(x)
     for r, n in ((out, "out"), (residual, "residual")):
-        if r is not None and (r.shape != x.shape or r.stride(1) != 1 or r.dtype != torch.float16):
-            raise ValueError(f"{n} must match x ([T, H] fp16, contiguous rows)")
+        if r is not None and (r.shape != x.shape or r.stride(1) != 1 or r.dtype != x.dtype):
+            raise ValueError(f"{n} must match x ([T, H], x's type, contiguous rows)")
     _lib.call("vaa_rmsnorm", x.data_ptr(), out.data_ptr(), weight.data_ptr(), _ptr(residual), t, h,
               x.stride(0), out.stride(0), residual.stride(0) if residual is not None else 0,
-              float(eps), _lib.stream_handle(stream))
+              float(eps), dt, _lib.stream_handle(stream))
     return out
 
 
@@ -458,10 +464,9 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
     """residual <- half(x + residual); out = rms_norm(residual) (vaa_add_rmsnorm).
     One pass for the reference layer's residual add, copy and norm
     (runner.py:1107-1130).  out may be x itself (the reference's in-place
-    hidden buffer) but not residual."""
+    hidden buffer) but not residual.  fp16 or bf16."""
     _require_gpu(x, residual, weight, out)
-    for t, n in ((x, "x"), (residual, "residual"), (weight, "weight")):
-        _require_dtype(t, torch.float16, n)
+    dt = _layer_dtype(x=x, residual=residual, weight=weight, out=out)
     if x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be [num_tokens, hidden] with contiguous rows")
     t, h = x.shape
@@ -470,11 +475,11 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
     if out is None:
         out = torch.empty_like(x)
     for r, n in ((out, "out"), (residual, "residual")):
-        if r.shape != x.shape or r.stride(1) != 1 or r.dtype != torch.float16:
-            raise ValueError(f"{n} must match x ([T, H] fp16, contiguous rows)")
+        if r.shape != x.shape or r.stride(1) != 1 or r.dtype != x.dtype:
+            raise ValueError(f"{n} must match x ([T, H], x's type, contiguous rows)")
     _lib.call("vaa_add_rmsnorm", x.data_ptr(), residual.data_ptr(), weight.data_ptr(),
               out.data_ptr(), t, h, x.stride(0), residual.stride(0), out.stride(0), float(eps),
-              _lib.stream_handle(stream))
+              dt, _lib.stream_handle(stream))
     return out
 
 
@@ -499,14 +504,14 @@ def rope_cos_sin_cache(rotary_dim: int, max_position: int, base: float,
 def rope_neox_(query: torch.Tensor, key: torch.Tensor | None, cos_cache: torch.Tensor,
                sin_cache: torch.Tensor, positions: torch.Tensor, *,
                rotary_dim: int | None = None, stream=None) -> None:
-    """In-place NeoX rotation of query [T, H, D] and key [T, KV, D]."""
+    """In-place NeoX rotation of query [T, H, D] and key [T, KV, D]; fp16 or bf16."""
     _require_gpu(query, key, cos_cache, sin_cache, positions)
-    _require_dtype(query, torch.float16, "query")
+    dt = _layer_dtype(query=query, key=key)
     if query.dim() != 3 or query.stride(2) != 1 or query.stride(1) != query.shape[2]:
         raise ValueError("query must be [T, H, D] with heads packed at stride D")
     if key is not None and (key.dim() != 3 or key.stride(2) != 1 or key.stride(1) != key.shape[2]
-                            or key.dtype != torch.float16 or key.shape[0] != query.shape[0]):
-        raise ValueError("key must be fp16 [T, KV, D] with heads packed at stride D")
+                            or key.shape[0] != query.shape[0]):
+        raise ValueError("key must be [T, KV, D] with heads packed at stride D")
     if positions.dtype != torch.int32 or not positions.is_contiguous():
         raise ValueError("positions must be a contiguous int32 tensor")
     t, h, d = query.shape
@@ -518,7 +523,7 @@ def rope_neox_(query: torch.Tensor, key: torch.Tensor | None, cos_cache: torch.T
     kv = key.shape[1] if key is not None else 0
     _lib.call("vaa_rope_neox", query.data_ptr(), _ptr(key), cos_cache.data_ptr(),
               sin_cache.data_ptr(), positions.data_ptr(), t, h, kv, d, rot, query.stride(0),
-              key.stride(0) if key is not None else 0, cos_cache.shape[0],
+              key.stride(0) if key is not None else 0, cos_cache.shape[0], dt,
               _lib.stream_handle(stream))
 
 
@@ -630,19 +635,19 @@ def topk_logits(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
              stream=None) -> torch.Tensor:
-    """out = half(silu(float(gate)) * float(up)); 1-D or row-strided 2-D views."""
+    """out = round16(silu(float(gate)) * float(up)); 1-D or row-strided 2-D views;
+    fp16 or bf16."""
     _require_gpu(gate, up, out)
-    for t, n in ((gate, "gate"), (up, "up")):
-        _require_dtype(t, torch.float16, n)
+    dt = _layer_dtype(gate=gate, up=up, out=out)
     if gate.shape != up.shape:
         raise ValueError("gate and up must have the same shape")
     if out is None:
-        out = torch.empty(gate.shape, dtype=torch.float16, device=gate.device)
-    if out.shape != gate.shape or out.dtype != torch.float16:
+        out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    if out.shape != gate.shape:
         raise ValueError("out must match gate")
     if gate.is_contiguous() and up.is_contiguous() and out.is_contiguous():
         _lib.call("vaa_silu_mul", gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
-                  _lib.stream_handle(stream))
+                  dt, _lib.stream_handle(stream))
         return out
     if gate.dim() != 2:
         raise ValueError("non-contiguous gate/up/out must be 2-D row-strided views")
@@ -651,7 +656,7 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = No
         if x.stride(-1) != 1:
             raise ValueError("last dimension must be contiguous")
     _lib.call("vaa_silu_mul_2d", g2.data_ptr(), u2.data_ptr(), o2.data_ptr(), g2.shape[0],
-              g2.shape[1], g2.stride(0), u2.stride(0), o2.stride(0), _lib.stream_handle(stream))
+              g2.shape[1], g2.stride(0), u2.stride(0), o2.stride(0), dt, _lib.stream_handle(stream))
     return out
 
 
