@@ -242,6 +242,13 @@ def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
 # each workgroup at least 32 tiles (512 tokens) and takes at most 8192
 # sequences.
 _DECODE_QUANTUM = 128
+# How much faster than its 1/CUs share of HBM one decode workgroup streams
+# when the launch leaves CUs idle.  Fitted on MI355X (32q/8kv D128 and C1):
+# with 2 the model picks the measured best partition for B=1 x 32768 (2048,
+# 35.1 us), B=1 x 8192 (512, 20.9 us), B=2 x 4096 (512, 17.3 us), B=4 x 1024
+# (256, 11.1 us) and C1 (unsplit, 7.0 us against 8.3 us with 128-token pieces
+# and the merge launch); 4 overshoots to pieces 2-4x too long.
+_LONE_WG_SPEEDUP = 2.0
 _BALANCED_MIN_TOKENS = 512
 _BALANCED_MAX_SEQS = 8192
 PARTITION_BALANCED = _lib.VAA_PARTITION_BALANCED
@@ -264,7 +271,10 @@ def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
     Fixed partitions of P tokens: the list-scheduling makespan
     max(total/m, largest piece) plus half a piece of tail when there is more
     than one wave of workgroups, a start-up cost per workgroup and, when any
-    sequence is split, the merge launch.  Balanced split: total/m plus one
+    sequence is split, the merge launch.  With fewer workgroups than CUs a
+    workgroup streams faster than its 1/m share of HBM: the largest piece is
+    scaled by 1/min(_LONE_WG_SPEEDUP, m/workgroups) (for tiny batches a merge
+    launch costs more than the split saves).  Balanced split: total/m plus one
     start-up per sequence piece a workgroup meets and the merge launch, which
     it always has.  Equal lengths that already cover the CUs stay unsplit;
     the balanced split must win by 3 % to be chosen.  Memoised per length
@@ -290,7 +300,8 @@ def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
     pieces = ((lens[None, :] + P[:, None] - 1) // P[:, None]).sum(axis=1)
     wgs = pieces * num_kv_heads
     big = np.minimum(P, longest).astype(np.float64)
-    t = np.maximum(total / m, big) + np.where(wgs > m, big / 2, 0.0) + wg_tokens * wgs / m
+    speed = np.clip(m / np.maximum(wgs, 1), 1.0, _LONE_WG_SPEEDUP)
+    t = np.maximum(total / m, big / speed) + np.where(wgs > m, big / 2, 0.0) + wg_tokens * wgs / m
     t = t + np.where(longest > P, merge_tokens, 0)
     i = int(np.argmin(t))
     best, t_fix = int(P[i]), float(t[i])
