@@ -124,6 +124,26 @@ def test_prefill_unwritten_rows(gpu):
     assert_close(out[w], ref[w], what="prefill valid rows")
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_prefill_invalid_block_mid_context(gpu, bs):
+    """An invalid entry inside the context aborts exactly the rows whose
+    context reaches it (paged_attention_v2.metal:428); earlier rows of the
+    same sequence are written, masked against the zero-filled block."""
+    kc, vc, bt, tok, pos, q = _prefill_case([1300, 150], [80, 60], 8, 2, 128, bs=bs, seed=11)
+    bad0 = 1250 // bs          # sequence 0: rows at positions >= bad0 * bs abort
+    bt[0, bad0] = -1
+    bad1 = 120 // bs           # sequence 1: an entry past num_blocks
+    bt[1, bad1] = kc.shape[0] + 3
+    out, ref, w = _run(kc, vc, bt, tok, pos, q)
+    p = pos.numpy()
+    t = tok.numpy()
+    expect = np.where(t == 0, p < bad0 * bs, p < bad1 * bs)
+    assert np.array_equal(w, expect)
+    assert w.any() and (~w).any()
+    assert np.all(out[~w] == np.float16(7.0))
+    assert_close(out[w], ref[w], what="prefill rows before an invalid block")
+
+
 def test_prefill_after_slot_write_c3_flow(gpu):
     """C3 flow: write the chunk's K/V through slot_mapping, then attend."""
     from vllm_apple_amd import kernels

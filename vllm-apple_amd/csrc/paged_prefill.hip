@@ -99,6 +99,22 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return v;
 }
 
+// max / sum of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the
+// upper half of its first operand with the lower half of its second, so with
+// x in both, one result holds x's lower half twice and the other its upper
+// half twice: a VALU exchange with no LDS round trip.  The sum adds the same
+// two values in both halves, so both hold the identical result.
+__device__ __forceinline__ float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::x4 lds_tr4(const f16* p) {
   const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -170,38 +186,56 @@ __device__ __forceinline__ void lanes_init(const PrefillArgs& a, int wave, int l
     L.vaddr[dt] = r * C::ROWB + ((4 * dt + 2 * (g16 & 1) + (j4 >> 1)) ^ sv) * 16 + (j4 & 1) * 8;
 }
 
-// Streams one 64-key tile into (kd, vd): wave w copies 16-key group w with
-// direct loads (or zeros for rows past the context / a missing block), and
-// every wave checks all four groups for the abort rule: a row whose context
-// [0, lim] reaches an invalid block is never written (paged_attention_v2.metal:428).
-template <int D>
-__device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* bts, int kvh,
-                                           int key0, int kv_len, int lim, int wave, int lane,
-                                           const Lanes<D>& L, BlockWindow& w, bool& aborted,
-                                           f16* kd, f16* vd) {
-  using C = PCfg<D>;
-  int64_t mine = -1;
-#pragma unroll
-  for (int h = 0; h < kWavesP; ++h) {
-    const int k0 = key0 + 16 * h;
-    if (k0 < kv_len) {
-      const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
-      const int64_t phys = window_block(a, bts, bi, w);
-      if (phys < 0 && k0 <= lim) aborted = true;
-      if (h == wave) mine = phys;
-    }
+// First key position of the sequence's context [0, kv_len) that lies in an
+// invalid block-table entry, or INT32_MAX.  A row whose context [0, lim]
+// reaches it is never written (paged_attention_v2.metal:428); checking this
+// once per sequence keeps the abort rule out of the tile loop.  The caller
+// guarantees ceil(kv_len / block_size) <= max_blocks.
+__device__ __forceinline__ int first_bad_key(const PrefillArgs& a, const int32_t* bts,
+                                             int kv_len, int lane) {
+  const int nb = (kv_len + a.block_size - 1) / a.block_size;
+  int bad = INT32_MAX;
+  for (int i = lane; i < nb; i += kWave) {
+    const int64_t e = bts[i];
+    if (e < 0 || e >= a.num_blocks) bad = min(bad, i);
   }
+  bad = wave_min_i(bad);
+  return bad == INT32_MAX ? INT32_MAX : bad * a.block_size;
+}
+
+// Streams one 64-key tile into (kd, vd): wave w copies 16-key group w with
+// direct loads, or zeros for rows past the context and for a missing block.
+// kbase / vbase point at this kv head's slice of block 0.
+template <int D>
+__device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* bts,
+                                           const char* kbase, const char* vbase, int key0,
+                                           int kv_len, int wave, int lane, const Lanes<D>& L,
+                                           BlockWindow& w, f16* kd, f16* vd) {
+  using C = PCfg<D>;
   const int k0 = key0 + 16 * wave;
-  const int nvalid = mine < 0 ? 0 : min(16, kv_len - k0);
+  int nvalid = 0, row0 = 0;
+  int64_t mine = -1;
+  if (k0 < kv_len) {
+    const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
+    mine = window_block(a, bts, bi, w);
+    row0 = k0 - bi * a.block_size;
+    if (mine >= 0) nvalid = min(16, kv_len - k0);
+  }
   char* kdst = reinterpret_cast<char*>(kd) + 1024 * (wave * C::NI);
   char* vdst = reinterpret_cast<char*>(vd) + 1024 * (wave * C::NI);
   if (nvalid > 0) {
-    const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
-    const int row0 = k0 - bi * a.block_size;
-    const char* kb = reinterpret_cast<const char*>(a.kc + mine * a.k_sb + kvh * a.k_sh +
-                                                   row0 * a.k_st);
-    const char* vb = reinterpret_cast<const char*>(a.vc + mine * a.v_sb + kvh * a.v_sh +
-                                                   row0 * a.v_st);
+    const char* kb = kbase + 2 * (mine * a.k_sb + static_cast<int64_t>(row0) * a.k_st);
+    const char* vb = vbase + 2 * (mine * a.v_sb + static_cast<int64_t>(row0) * a.v_st);
+    if (nvalid == 16) {  // every tile but a sequence's last
+#pragma unroll
+      for (int q = 0; q < C::NI; ++q) {
+        __builtin_amdgcn_global_load_lds((gbl_void_t*)(kb + L.koff[q]),
+                                         (lds_void_t*)(kdst + 1024 * q), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((gbl_void_t*)(vb + L.voff[q]),
+                                         (lds_void_t*)(vdst + 1024 * q), 16, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < C::NI; ++q) {
       if (L.row[q] < nvalid) {
@@ -268,7 +302,7 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
   float mx = -INFINITY;
 #pragma unroll
   for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sacc[0][r], sacc[1][r]));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * a.scale_log2;
+  mx = half_max(mx) * a.scale_log2;
   // Lazy rescale: keep the reference max unless a score exceeds it by more
   // than 2^8 (p stays <= 256, exact in fp16); the wave-uniform branch is
   // taken on a row's first tile and on rare outliers only.  Only lanes whose
@@ -374,6 +408,8 @@ paged_prefill_kernel(PrefillArgs a) {
 
   Lanes<D> L;
   lanes_init<D>(a, wave, lane, L);
+  const char* kbase = reinterpret_cast<const char*>(a.kc + kvh * a.k_sh);
+  const char* vbase = reinterpret_cast<const char*>(a.vc + kvh * a.v_sh);
 
   while (true) {
     // Next sequence among the workgroup's unfinished tokens, and its context.
@@ -394,25 +430,26 @@ paged_prefill_kernel(PrefillArgs a) {
     const int n_kt = (kv_len + kKT - 1) / kKT;
     const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
     const int lim = active ? tpos : -1;  // last key position this row may see
+    if (lim >= first_bad_key(a, bts, kv_len, lane)) aborted = true;
 
     // Double buffer: the next tile's direct loads are issued before this
     // tile's math; one wait + barrier per tile publishes it.
     BlockWindow win;
     window_load(a, bts, 0, win);
-    tile_fetch<D>(a, bts, kvh, 0, kv_len, lim, wave, lane, L, win, aborted, k0s, v0s);
+    tile_fetch<D>(a, bts, kbase, vbase, 0, kv_len, wave, lane, L, win, k0s, v0s);
     wait_all();
     __builtin_amdgcn_s_barrier();
     for (int kt = 0; kt < n_kt; kt += 2) {
       if (kt + 1 < n_kt)
-        tile_fetch<D>(a, bts, kvh, (kt + 1) * kKT, kv_len, lim, wave, lane, L, win, aborted,
-                      k1s, v1s);
+        tile_fetch<D>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
+                      v1s);
       if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
       wait_all();
       __builtin_amdgcn_s_barrier();
       if (kt + 1 >= n_kt) break;
       if (kt + 2 < n_kt)
-        tile_fetch<D>(a, bts, kvh, (kt + 2) * kKT, kv_len, lim, wave, lane, L, win, aborted,
-                      k0s, v0s);
+        tile_fetch<D>(a, bts, kbase, vbase, (kt + 2) * kKT, kv_len, wave, lane, L, win, k0s,
+                      v0s);
       if (math) tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
       wait_all();
       __builtin_amdgcn_s_barrier();
@@ -421,7 +458,7 @@ paged_prefill_kernel(PrefillArgs a) {
   }
 
   if (!math) return;
-  const float l_tot = l_part + __shfl_xor(l_part, 32, kWave);
+  const float l_tot = half_sum(l_part);
   if (!row_ok || aborted) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   f16* op = a.out + static_cast<int64_t>(tok) * a.o_st + head * a.o_sh;
