@@ -512,6 +512,25 @@ paged_decode_balanced_kernel(DecodeArgs a) {
 // starts[seq]/per .. (starts[seq+1]-1)/per of its kv head; when that is one
 // workgroup the decode kernel wrote the row already.  Rows of empty
 // sequences are zeroed here.
+// Log-sum-exp merge of split partials (m_p, l_p, acc_p) in one pass:
+//   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p,
+// kept as a running maximum with the sums rescaled when it grows, so each
+// piece's three loads are independent of the others and issue together.
+// Pieces with l_p = 0 (nothing visible) are skipped.
+struct MergeAcc {
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  __device__ __forceinline__ void add(float mp, float lp, float ap) {
+    if (!(lp > 0.f)) return;
+    const float Mn = fmaxf(M, mp);
+    const float so = fast_exp2(M - Mn);  // 0 while M = -inf
+    const float sn = fast_exp2(mp - Mn);
+    num = num * so + ap * sn;
+    den = den * so + lp * sn;
+    M = Mn;
+  }
+  __device__ __forceinline__ float value() const { return den > 0.f ? num / den : 0.f; }
+};
+
 template <int D, typename T>
 __global__ void __launch_bounds__(D)
 paged_decode_merge_balanced_kernel(DecodeArgs a) {
@@ -527,24 +546,13 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
   if (c0 == c1) return;
   const int kvh = qh / G, h = qh % G;
   const int64_t base = static_cast<int64_t>(kvh) * (nc + B) + seq;
-  float M = -INFINITY;
+  MergeAcc m;
+#pragma unroll 4
   for (int c = c0; c <= c1; ++c) {
     const int64_t row = (base + c) * G + h;
-    if (a.ws_ml[row * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[row * 2]);
+    m.add(a.ws_ml[row * 2], a.ws_ml[row * 2 + 1], a.ws_acc[row * D + d]);
   }
-  float num = 0.f, den = 0.f;
-  if (M != -INFINITY) {
-    for (int c = c0; c <= c1; ++c) {
-      const int64_t row = (base + c) * G + h;
-      const float lp = a.ws_ml[row * 2 + 1];
-      if (!(lp > 0.f)) continue;
-      const float sc = fast_exp2(a.ws_ml[row * 2] - M);
-      num += sc * a.ws_acc[row * D + d];
-      den += sc * lp;
-    }
-  }
-  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
-      Elem<T>::from_f(den > 0.f ? num / den : 0.f);
+  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(m.value());
 }
 
 // Second pass for split sequences:
@@ -561,22 +569,11 @@ paged_decode_merge_kernel(DecodeArgs a) {
   const int n_parts = min((L + part_tok - 1) / part_tok, a.max_parts);
   if (n_parts <= 1) return;  // written directly by the decode kernel
   const int64_t row0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh) * a.max_parts;
-  float M = -INFINITY;
-  for (int p = 0; p < n_parts; ++p) {
-    if (a.ws_ml[(row0 + p) * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[(row0 + p) * 2]);
-  }
-  float num = 0.f, den = 0.f;
-  if (M != -INFINITY) {
-    for (int p = 0; p < n_parts; ++p) {
-      const float lp = a.ws_ml[(row0 + p) * 2 + 1];
-      if (!(lp > 0.f)) continue;
-      const float sc = fast_exp2(a.ws_ml[(row0 + p) * 2] - M);
-      num += sc * a.ws_acc[(row0 + p) * D + d];
-      den += sc * lp;
-    }
-  }
-  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
-      Elem<T>::from_f(den > 0.f ? num / den : 0.f);
+  MergeAcc m;
+#pragma unroll 8
+  for (int p = 0; p < n_parts; ++p)
+    m.add(a.ws_ml[(row0 + p) * 2], a.ws_ml[(row0 + p) * 2 + 1], a.ws_acc[(row0 + p) * D + d]);
+  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(m.value());
 }
 
 int g_num_cus = 0;
