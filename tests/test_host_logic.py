@@ -199,15 +199,18 @@ def test_ops_reject_cpu_tensors():
 
 def test_partition_choice_small_batches():
     """Split-K choices the cost model makes where the launch leaves CUs idle,
-    each the fastest of the partitions measured on MI355X (kernels.py,
-    _LONE_WG_SPEEDUP), and the headline / ragged choices unchanged."""
+    each the fastest (or within 6 %) of the partitions measured on MI355X
+    (kernels.py, _LONE_WG_SPEEDUP), and the headline / ragged choices
+    unchanged."""
     from vllm_apple_amd import kernels as K
 
     K._partition_cache.clear()
-    assert K.choose_partition_size([32768], 8, 256) == 2048
-    assert K.choose_partition_size([8192], 8, 256) == 512
-    assert K.choose_partition_size([4096] * 2, 8, 256) == 512
-    assert K.choose_partition_size([1024] * 4, 8, 256) == 256
+    assert K.choose_partition_size([8192], 8, 256) == 256
+    assert K.choose_partition_size([4096] * 2, 8, 256) == 256
+    assert K.choose_partition_size([2048] * 8, 8, 256) == 512
+    assert K.choose_partition_size([1024] * 4, 8, 256) == 128
+    assert K.choose_partition_size([4096] * 16, 8, 256) == 1024
+    assert K.choose_partition_size([32768], 8, 256) == 1024
     assert K.choose_partition_size([162, 125, 444, 341], 2, 256) >= 444  # C1: unsplit
     assert K.choose_partition_size([8192] * 32, 8, 256) == 8192          # headline: unsplit
     assert K.choose_partition_size(list(range(1024, 8192, 224)), 8, 256) == K.PARTITION_BALANCED

@@ -43,6 +43,7 @@ namespace vaa {
 namespace {
 
 constexpr int kWaves = 8;   // waves per workgroup
+constexpr int kShortPartTiles = 64;  // fixed partitions up to 1024 tokens run 4-wave workgroups
 constexpr int kTile = 16;   // tokens per MFMA tile
 
 // Tensors are raw 16-bit storage; the kernels' element type T (fp16 or bf16)
@@ -196,12 +197,12 @@ struct RangeOut {
   int64_t prow_step;  // workspace row stride between the group's query heads
 };
 
-// The 8 waves of the workgroup attend query heads kvh*G .. kvh*G+G-1 of
+// The NW waves of the workgroup attend query heads kvh*G .. kvh*G+G-1 of
 // sequence seq over the 16-token tiles [t0, t1) of its first L (clamped)
 // positions: each wave streams a contiguous run of tiles, then the waves
 // combine through LDS.  smem is reused on return only after the trailing
 // barrier, so a workgroup may call this repeatedly.
-template <int D, typename T>
+template <int D, typename T, int NW = kWaves>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int L, bool fused, int t0, int t1,
                                              const RangeOut& ro, bool trailing_barrier) {
@@ -210,7 +211,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   const int c16 = lane & 15, g = lane >> 4;
   const int G = a.G;
   const int n_tiles = (L + kTile - 1) / kTile;
-  const int per = (t1 - t0 + kWaves - 1) / kWaves;
+  const int per = (t1 - t0 + NW - 1) / NW;
   const int jb = t0 + wave * per;
   const int je = min(jb + per, t1);
 
@@ -334,8 +335,8 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   // Cross-wave combine through LDS: wm/wl [wave][16], wa [wave][G][D].
   __syncthreads();
   float* wm = reinterpret_cast<float*>(smem);
-  float* wl = wm + kWaves * 16;
-  float* wa = wl + kWaves * 16;
+  float* wl = wm + NW * 16;
+  float* wa = wl + NW * 16;
   if (c16 < G) {
     if (g == 0) {
       wm[wave * 16 + c16] = m_run;
@@ -356,11 +357,11 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w * 16 + h]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w * 16 + h]);
     float num = 0.f, den = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float mw = wm[w * 16 + h];
         if (mw == -INFINITY) continue;
         const float sc = fast_exp2(mw - M);
@@ -399,9 +400,11 @@ __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int seq) {
   return L > cap ? cap : L;
 }
 
-// Fixed partitions: grid (partition, kv_head, seq).
-template <int D, typename T>
-__global__ void __launch_bounds__(kWaves* kWave)
+// Fixed partitions: grid (partition, kv_head, seq).  NW waves per workgroup:
+// 8 for long partitions; 4 for short ones, so that two workgroups share a CU
+// and one's start-up (Q load, first tiles) overlaps the other's tail.
+template <int D, typename T, int NW>
+__global__ void __launch_bounds__(NW* kWave)
 paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
@@ -422,7 +425,8 @@ paged_decode_kernel(DecodeArgs a) {
   ro.whole = (n_parts == 1);
   ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + kvh * G) * a.max_parts + part;
   ro.prow_step = a.max_parts;
-  decode_range<D, T>(a, smem, seq, kvh, L, a.new_k != nullptr && Lorig == L, t0, t1, ro, false);
+  decode_range<D, T, NW>(a, smem, seq, kvh, L, a.new_k != nullptr && Lorig == L, t0, t1, ro,
+                         false);
 }
 
 // Balanced split: the tiles of all sequences (for one kv head) are laid end
@@ -712,7 +716,17 @@ int launch_decode(const DecodeArgs& a0, bool balanced, hipStream_t stream) {
     return check_launch("paged_decode_merge_balanced_kernel");
   }
   dim3 grid(a.max_parts, a.num_kv_heads, a.num_seqs);
-  hipLaunchKernelGGL((paged_decode_kernel<D, T>), grid, dim3(kWaves * kWave), lds, stream, a);
+  if (a.max_parts > 1 && a.part_tiles <= kShortPartTiles) {
+    constexpr int kNw = kWaves / 2;
+    const size_t lds4 = std::max(static_cast<size_t>(kNw) * kTile * D * sizeof(f16),
+                                 (2 * kNw * 16 + static_cast<size_t>(kNw) * a.G * D) *
+                                     sizeof(float));
+    hipLaunchKernelGGL((paged_decode_kernel<D, T, kNw>), grid, dim3(kNw * kWave), lds4, stream,
+                       a);
+  } else {
+    hipLaunchKernelGGL((paged_decode_kernel<D, T, kWaves>), grid, dim3(kWaves * kWave), lds,
+                       stream, a);
+  }
   int st = check_launch("paged_decode_kernel");
   if (st || a.max_parts <= 1) return st;
   hipLaunchKernelGGL((paged_decode_merge_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs), dim3(D),

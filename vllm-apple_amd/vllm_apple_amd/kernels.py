@@ -237,18 +237,24 @@ def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
     return int(n), int(part.value)
 
 
-# Decode launch geometry (paged_decode.hip): one workgroup of 8 waves per CU
-# at a time, partitions in multiples of 128 tokens; the balanced split gives
-# each workgroup at least 32 tiles (512 tokens) and takes at most 8192
-# sequences.
+# Decode launch geometry (paged_decode.hip): partitions in multiples of 128
+# tokens; partitions up to 1024 tokens run 4-wave workgroups, two per CU (one's
+# start-up overlaps the other's streaming), longer ones and the balanced split
+# one 8-wave workgroup per CU.  The balanced split gives each workgroup at
+# least 32 tiles (512 tokens) and takes at most 8192 sequences.
 _DECODE_QUANTUM = 128
-# How much faster than its 1/CUs share of HBM one decode workgroup streams
-# when the launch leaves CUs idle.  Fitted on MI355X (32q/8kv D128 and C1):
-# with 2 the model picks the measured best partition for B=1 x 32768 (2048,
-# 35.1 us), B=1 x 8192 (512, 20.9 us), B=2 x 4096 (512, 17.3 us), B=4 x 1024
-# (256, 11.1 us) and C1 (unsplit, 7.0 us against 8.3 us with 128-token pieces
-# and the merge launch); 4 overshoots to pieces 2-4x too long.
-_LONE_WG_SPEEDUP = 2.0
+_SHORT_PART_TOKENS = 1024
+# How much faster than its share of HBM a decode workgroup streams when the
+# launch leaves slots idle (8-wave: one slot per CU; 4-wave: two, each half a
+# CU's share), and the start-up of a 4-wave workgroup relative to an 8-wave
+# one.  Fitted on MI355X (32q/8kv D128; us per step, measured best in
+# brackets): the model picks B=1 x 8192 -> 256 (20.6 [19.6 at 512]),
+# B=2 x 4096 -> 256 (16.7), B=8 x 2048 -> 512 (19.3), B=4 x 1024 -> 128
+# (10.8), B=16 x 4096 -> 1024 (47.4; unsplit 54.1), B=1 x 32768 -> 1024
+# (37.5 [33.4 at 2048]); C1 and the headline stay unsplit.
+_LONE_WG_SPEEDUP = 1.7
+_SHORT_WG_SPEEDUP = 2.0
+_SHORT_START = 0.5
 _BALANCED_MIN_TOKENS = 512
 _BALANCED_MAX_SEQS = 8192
 PARTITION_BALANCED = _lib.VAA_PARTITION_BALANCED
@@ -271,10 +277,12 @@ def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
     Fixed partitions of P tokens: the list-scheduling makespan
     max(total/m, largest piece) plus half a piece of tail when there is more
     than one wave of workgroups, a start-up cost per workgroup and, when any
-    sequence is split, the merge launch.  With fewer workgroups than CUs a
-    workgroup streams faster than its 1/m share of HBM: the largest piece is
-    scaled by 1/min(_LONE_WG_SPEEDUP, m/workgroups) (for tiny batches a merge
-    launch costs more than the split saves).  Balanced split: total/m plus one
+    sequence is split, the merge launch.  With fewer workgroups than slots a
+    workgroup streams faster than its share of HBM: the largest piece is
+    scaled by 1/min(speed-up cap, slots/workgroups).  Short partitions (at
+    most _SHORT_PART_TOKENS) run two 4-wave workgroups per CU, each with half
+    a CU's share and a cheaper start-up (for tiny batches a merge launch
+    costs more than the split saves).  Balanced split: total/m plus one
     start-up per sequence piece a workgroup meets and the merge launch, which
     it always has.  Equal lengths that already cover the CUs stay unsplit;
     the balanced split must win by 3 % to be chosen.  Memoised per length
@@ -300,8 +308,13 @@ def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
     pieces = ((lens[None, :] + P[:, None] - 1) // P[:, None]).sum(axis=1)
     wgs = pieces * num_kv_heads
     big = np.minimum(P, longest).astype(np.float64)
-    speed = np.clip(m / np.maximum(wgs, 1), 1.0, _LONE_WG_SPEEDUP)
-    t = np.maximum(total / m, big / speed) + np.where(wgs > m, big / 2, 0.0) + wg_tokens * wgs / m
+    # Split into short partitions: 4-wave workgroups, two slots per CU.
+    short = (P <= _SHORT_PART_TOKENS) & (longest > P)
+    slots = np.where(short, 2 * m, m)
+    cap = np.where(short, _SHORT_WG_SPEEDUP, _LONE_WG_SPEEDUP)
+    speed = np.clip(slots / np.maximum(wgs, 1), 1.0, cap) / np.where(short, 2.0, 1.0)
+    start = wg_tokens * np.where(short, _SHORT_START, 1.0) * wgs / m
+    t = np.maximum(total / m, big / speed) + np.where(wgs > slots, big / 2, 0.0) + start
     t = t + np.where(longest > P, merge_tokens, 0)
     i = int(np.argmin(t))
     best, t_fix = int(P[i]), float(t[i])
