@@ -459,7 +459,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+                                   "(multi-GPU sharding is described, not built)"}))
         return 2
     import torch
 
