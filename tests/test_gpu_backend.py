@@ -315,3 +315,48 @@ def test_kv_cache_object_write_and_validate(gpu):
     assert int(torch.count_nonzero(c.get_key_buffer(0))) == 0
     with pytest.raises(ValueError):
         c.write_kv(0, 0, 16, torch.from_numpy(key), torch.from_numpy(val))
+
+
+def test_forward_mixed_overlap_matches_serial_and_graph_replays(gpu, monkeypatch):
+    """A mixed step runs prefill (side stream) and decode (current stream)
+    concurrently: bit-identical to running them in turn, and a HIP graph of
+    the step replays to the eager result every time (with eager work and
+    synchronizations between the replays)."""
+    from vllm_apple_amd import backend as B
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    b = _mixed_batch(seed=9)
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    impl = HipAttentionImpl(H, D, 1 / math.sqrt(D), KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv = b["qkv"].to(dev)
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    md = _metadata(b, dev)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv(B.OVERLAP_ENV, mode)
+        kv_cache = b["kv_cache"].to(dev)
+        out = torch.zeros((T, H, D), dtype=torch.float16, device=dev)
+        impl.forward(None, q, k, v, kv_cache, md, output=out)
+        torch.cuda.synchronize()
+        outs[mode] = (out.clone(), kv_cache.clone())
+    assert torch.equal(outs["0"][0], outs["1"][0])
+    assert torch.equal(outs["0"][1], outs["1"][1])
+    # Graph capture of the overlapped step (the KV write is idempotent).
+    monkeypatch.setenv(B.OVERLAP_ENV, "1")
+    kv_cache = b["kv_cache"].to(dev)
+    out = torch.zeros((T, H, D), dtype=torch.float16, device=dev)
+    impl.forward(None, q, k, v, kv_cache, md, output=out)  # warm-up (workspaces)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        impl.forward(None, q, k, v, kv_cache, md, output=out)
+    for r in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, outs["1"][0]), f"replay {r}"
+        _ = (out.float() * 2).sum().item()  # eager work between replays

@@ -19,6 +19,7 @@ for AttentionType and the abstract bases.
 from __future__ import annotations
 
 import logging
+import os
 from dataclasses import dataclass
 from typing import Any, ClassVar, Optional
 
@@ -182,6 +183,15 @@ class HipAttentionMetadataBuilder:
         )
 
 
+OVERLAP_ENV = "VLLM_VAA_OVERLAP"
+
+
+def _overlap_enabled() -> bool:
+    """Decode and prefill of a mixed step run concurrently unless
+    VLLM_VAA_OVERLAP=0."""
+    return os.environ.get(OVERLAP_ENV, "1") != "0"
+
+
 class HipAttentionImpl(AttentionImpl):
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
                  alibi_slopes: Optional[list], sliding_window: Optional[int],
@@ -276,7 +286,8 @@ class HipAttentionImpl(AttentionImpl):
                 kernels.kv_write_slots(key[:n], value[:n], key_cache, value_cache,
                                        attn_metadata.slot_mapping[:n], layout="vllm")
             nd = attn_metadata.num_decode_tokens
-            if nd > 0:
+
+            def decode():
                 # Host lengths, only if already cached (never a device sync here).
                 lens_host = attn_metadata._seq_lens_cpu
                 kernels.paged_decode(query[:nd], key_cache, value_cache,
@@ -285,12 +296,24 @@ class HipAttentionImpl(AttentionImpl):
                                      max_seq_len=attn_metadata.max_seq_len, layout="vllm",
                                      output=output[:nd],
                                      seq_lens_host=lens_host[:nd] if lens_host else None)
-            if n > nd:
-                tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,
-                                                     attn_metadata.seq_lens, n)
+
+            def prefill():
                 kernels.paged_prefill(query[nd:n], key_cache, value_cache,
                                       attn_metadata.block_table, tok[nd:n], pos[nd:n],
                                       scale=self.scale, layout="vllm", output=output[nd:n])
+
+            if n > nd:
+                tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,
+                                                     attn_metadata.seq_lens, n)
+            if nd > 0 and n > nd and _overlap_enabled():
+                # Mixed step: prefill (MFMA) and decode (HBM) run concurrently;
+                # the results are bit-identical to running them in turn.
+                kernels.overlap(prefill, decode, query.device)
+            else:
+                if nd > 0:
+                    decode()
+                if n > nd:
+                    prefill()
         if conv:
             original_output[:n].copy_(output[:n].to(original_output.dtype))
             return original_output
