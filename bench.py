@@ -309,10 +309,10 @@ def wl_c5(args) -> dict:
     out = torch.empty_like(b.query)
     lens = b.extra["seq_lens_host"]
 
-    def decode():
+    def decode(shared=False):
         kernels.paged_decode(b.query[:nd], b.k_cache, b.v_cache, b.block_table[:nd],
                              b.seq_lens[:nd], scale=b.scale, max_seq_len=max(lens[:nd]),
-                             output=out[:nd], seq_lens_host=lens[:nd])
+                             output=out[:nd], seq_lens_host=lens[:nd], shared=shared)
 
     def prefill():
         kernels.paged_prefill(b.query[nd:], b.k_cache, b.v_cache, b.block_table,
@@ -323,7 +323,7 @@ def wl_c5(args) -> dict:
         # As the backend runs a mixed step: the KV write, then prefill (side
         # stream) and decode (current stream) concurrently.
         kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache, b.slot_mapping)
-        kernels.overlap(prefill, decode, dev)
+        kernels.overlap(prefill, lambda: decode(shared=True), dev)
 
     def attn_step_serial():
         kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache, b.slot_mapping)

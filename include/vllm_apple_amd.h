@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define VAA_ABI_VERSION 3
+#define VAA_ABI_VERSION 4
 
 enum {
   VAA_OK = 0,
@@ -61,8 +61,14 @@ enum { VAA_DTYPE_F16 = 0, VAA_DTYPE_BF16 = 1 };
  *   VAA_PARTITION_BALANCED  one workgroup per CU, each taking an equal share
  *        of the 16-token tiles of all sequences, split on the device from
  *        seq_lens (for unequal lengths; at most 8192 sequences).
+ *   VAA_PARTITION_BALANCED_SHARED  the same split over workgroups of half the
+ *        size, two per CU, for a decode that runs concurrently with another
+ *        kernel (a mixed step's prefill on a second stream): its workgroups
+ *        then share CUs with the other kernel's instead of waiting for them.
+ *        Slower than VAA_PARTITION_BALANCED when decode runs alone.
  */
 #define VAA_PARTITION_BALANCED (-1)
+#define VAA_PARTITION_BALANCED_SHARED (-2)
 
 /*
  * Attention parameters.  Mirrors FusedAttentionParams / PagedAttentionParams
@@ -81,7 +87,8 @@ typedef struct vaa_attn_params {
   int32_t num_query_heads;
   int32_t queries_per_kv;     /* num_query_heads / num_kv_heads, <= 16        */
   int32_t partition_size;     /* split-K tokens per partition; 0 = automatic,
-                                 VAA_PARTITION_BALANCED = split by lengths    */
+                                 VAA_PARTITION_BALANCED(_SHARED) = split by
+                                 lengths                                      */
   int64_t num_blocks;         /* cache capacity in blocks                     */
   int64_t k_stride_block, k_stride_head, k_stride_token;
   int64_t v_stride_block, v_stride_head, v_stride_token;

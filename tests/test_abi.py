@@ -77,7 +77,7 @@ def test_params_struct_layout_matches_header(tmp_path):
 
 
 def test_version_and_error_string_without_gpu(lib):
-    assert lib.vaa_abi_version() == 3
+    assert lib.vaa_abi_version() == 4
     from vllm_apple_amd import _lib
 
     assert isinstance(_lib.last_error(), str)
@@ -220,3 +220,25 @@ def test_layer_op_dtype_errors(lib):
                              None) == _lib.VAA_ERR_UNSUPPORTED
     assert lib.vaa_silu_mul(a, a, a, 16, -1, None) == _lib.VAA_ERR_UNSUPPORTED
     assert lib.vaa_silu_mul_2d(a, a, a, 2, 16, 16, 16, 16, 3, None) == _lib.VAA_ERR_UNSUPPORTED
+
+
+def test_balanced_shared_workspace(lib):
+    """The shared balanced split plans two workgroups per CU: its workspace
+    holds more partial rows than the one-per-CU split; other negative
+    partition sizes are refused."""
+    from vllm_apple_amd import _lib
+
+    p = _lib.VaaAttnParams()
+    p.head_size, p.block_size, p.num_kv_heads, p.num_query_heads = 128, 16, 8, 32
+    p.queries_per_kv, p.num_seqs, p.max_blocks_per_seq, p.num_blocks = 4, 56, 1024, 8192
+    p.max_seq_len = 16384
+    part = ctypes.c_int32(0)
+    p.partition_size = _lib.VAA_PARTITION_BALANCED
+    one = lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part))
+    assert part.value == _lib.VAA_PARTITION_BALANCED
+    p.partition_size = _lib.VAA_PARTITION_BALANCED_SHARED
+    two = lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part))
+    assert part.value == _lib.VAA_PARTITION_BALANCED_SHARED
+    assert two > one > 0
+    p.partition_size = -3
+    assert lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part)) == 0

@@ -175,19 +175,21 @@ def test_decode_matches_pure_loop_oracle(gpu):
     assert_close(host(out), loop, what="vs Metal-structured loop")
 
 
+@pytest.mark.parametrize("mode", [-1, -2])
 @pytest.mark.parametrize("seed", [21, 22])
-def test_decode_balanced_ragged_batch(gpu, seed):
+def test_decode_balanced_ragged_batch(gpu, seed, mode):
     """Balanced split over many ragged sequences (empty ones included): every
     piece boundary (inside a sequence, between sequences, across workgroups)
-    against the oracle, with the fused write bit-exact."""
+    against the oracle, with the fused write bit-exact.  mode -1 is one
+    8-wave workgroup per CU, -2 (shared) two 4-wave workgroups per CU."""
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(0, 3000, (77,), generator=g)
     lens[::9] = 0
     lens[5] = 1
     lens = lens.tolist()
-    print(f"[case] balanced ragged seed={seed}", flush=True)
+    print(f"[case] balanced ragged seed={seed} mode={mode}", flush=True)
     kc, vc, bt, L, q, nk, nv = _case(77, 16, 4, 128, lens, seed=seed)
-    out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=-1)
+    out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=mode)
     assert_close(host(out), ref, what="balanced ragged")
     assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
     assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16))
@@ -207,6 +209,6 @@ def test_decode_balanced_workspace_reuse(gpu):
         kc, vc, bt, L, q, nk, nv = _case(S, 32, 8, 128, lens, seed=seed)
         out = kernels.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), L.cuda(),
                                    scale=1 / np.sqrt(128), max_seq_len=max(lens),
-                                   partition_size=-1, workspace=ws)
+                                   partition_size=-2 if S == 7 else -1, workspace=ws)
         ref = oat.decode(host(q), host(kc), host(vc), host(bt), host(L), 1 / np.sqrt(128))
         assert_close(host(out), ref, what=f"balanced reuse S={S}")

@@ -44,6 +44,8 @@ namespace {
 
 constexpr int kWaves = 8;   // waves per workgroup
 constexpr int kShortPartTiles = 64;  // fixed partitions up to 1024 tokens run 4-wave workgroups
+constexpr int kSharedWaves = kWaves / 2;  // VAA_PARTITION_BALANCED_SHARED: 4-wave workgroups,
+                                          // two per CU
 constexpr int kTile = 16;   // tokens per MFMA tile
 
 // Tensors are raw 16-bit storage; the kernels' element type T (fp16 or bf16)
@@ -472,8 +474,8 @@ __device__ __forceinline__ void tile_prefix(const DecodeArgs& a, int* starts, in
   __syncthreads();
 }
 
-template <int D, typename T>
-__global__ void __launch_bounds__(kWaves* kWave)
+template <int D, typename T, int NW>
+__global__ void __launch_bounds__(NW* kWave)
 paged_decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int c = blockIdx.x, kvh = blockIdx.y, nc = gridDim.x;
@@ -506,8 +508,8 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(kvh) * (nc + B) + c + seq) * G;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T>(a, smem, seq, kvh, L, a.new_k != nullptr && a.seq_lens[seq] == L, t0, t1,
-                    ro, true);
+    decode_range<D, T, NW>(a, smem, seq, kvh, L, a.new_k != nullptr && a.seq_lens[seq] == L, t0,
+                           t1, ro, true);
     pos = s0 + t1;
   }
 }
@@ -598,6 +600,7 @@ constexpr int kBalMaxSeqs = 8192;  // prefix sums of tiles per sequence live in 
 // How a call splits its sequences.
 struct Split {
   bool balanced;     // balanced split over the actual lengths
+  bool shared;       // balanced over 4-wave workgroups, two per CU
   int part;          // fixed: tokens per partition (balanced: -1)
   int max_parts;     // fixed: partitions per sequence; balanced: workgroups per kv head
   size_t ws_bytes;   // workspace needed (0: none)
@@ -609,7 +612,8 @@ struct Split {
 // as needed for the workgroups to cover every CU once, in multiples of
 // 16 * kWaves tokens.  VAA_PARTITION_BALANCED: one workgroup per CU, each
 // taking an equal share of the tiles of all sequences (split on the device
-// from seq_lens).
+// from seq_lens); VAA_PARTITION_BALANCED_SHARED: the same over two 4-wave
+// workgroups per CU.
 int plan_split(const vaa_attn_params* p, Split* sp) {
   const int64_t cap = static_cast<int64_t>(p->max_blocks_per_seq) * p->block_size;
   int64_t max_len = p->max_seq_len;
@@ -618,13 +622,16 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
   const int quantum = kTile * kWaves;
   int64_t part = p->partition_size;
   const size_t row_bytes = (static_cast<size_t>(p->head_size) + 2) * sizeof(float);
-  if (part == VAA_PARTITION_BALANCED) {
+  if (part == VAA_PARTITION_BALANCED || part == VAA_PARTITION_BALANCED_SHARED) {
     if (p->num_seqs > kBalMaxSeqs)
       return fail(VAA_ERR_UNSUPPORTED, "balanced split: num_seqs=%d > %d", p->num_seqs,
                   kBalMaxSeqs);
-    const int wgs = (num_cus() + p->num_kv_heads - 1) / p->num_kv_heads;
+    const bool shared = part == VAA_PARTITION_BALANCED_SHARED;
+    const int per_cu = shared ? kWaves / kSharedWaves : 1;
+    const int wgs = (per_cu * num_cus() + p->num_kv_heads - 1) / p->num_kv_heads;
     sp->balanced = true;
-    sp->part = VAA_PARTITION_BALANCED;
+    sp->shared = shared;
+    sp->part = static_cast<int>(part);
     sp->max_parts = wgs < 1 ? 1 : wgs;
     sp->hdr_bytes = ((static_cast<size_t>(p->num_seqs) + 2) * sizeof(int) + 255) / 256 * 256;
     const size_t rows = static_cast<size_t>(p->num_kv_heads) * (sp->max_parts + p->num_seqs) *
@@ -644,11 +651,12 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
     part = (max_len + splits - 1) / splits;
     part = (part + quantum - 1) / quantum * quantum;
   } else {
-    return fail(VAA_ERR_INVALID_ARG, "partition_size=%lld (use > 0, 0 or %d)",
-                (long long)part, VAA_PARTITION_BALANCED);
+    return fail(VAA_ERR_INVALID_ARG, "partition_size=%lld (use > 0, 0, %d or %d)",
+                (long long)part, VAA_PARTITION_BALANCED, VAA_PARTITION_BALANCED_SHARED);
   }
   if (part > (int64_t{1} << 30)) part = int64_t{1} << 30;
   sp->balanced = false;
+  sp->shared = false;
   sp->part = static_cast<int>(part);
   sp->max_parts = static_cast<int>((max_len + part - 1) / part);
   sp->hdr_bytes = 0;
@@ -698,17 +706,27 @@ int check_params(const vaa_attn_params* p, const char* what) {
 }
 
 template <int D, typename T>
-int launch_decode(const DecodeArgs& a0, bool balanced, hipStream_t stream) {
+int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t stream) {
   DecodeArgs a = a0;
   const size_t lds_tiles = static_cast<size_t>(kWaves) * kTile * D * sizeof(f16);
   const size_t lds_comb =
       (2 * kWaves * 16 + static_cast<size_t>(kWaves) * a.G * D) * sizeof(float);
   const size_t lds = lds_tiles > lds_comb ? lds_tiles : lds_comb;
   if (balanced) {
-    a.lds_main = static_cast<int>((lds + 15) / 16 * 16);
+    const int nw = shared ? kSharedWaves : kWaves;
+    const size_t lds_bal =
+        std::max(static_cast<size_t>(nw) * kTile * D * sizeof(f16),
+                 (2 * nw * 16 + static_cast<size_t>(nw) * a.G * D) * sizeof(float));
+    a.lds_main = static_cast<int>((lds_bal + 15) / 16 * 16);
     const size_t lds_b = a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kWaves) * sizeof(int);
-    hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T>), dim3(a.max_parts, a.num_kv_heads),
-                       dim3(kWaves * kWave), lds_b, stream, a);
+    if (shared)
+      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kSharedWaves>),
+                         dim3(a.max_parts, a.num_kv_heads), dim3(kSharedWaves * kWave), lds_b,
+                         stream, a);
+    else
+      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kWaves>),
+                         dim3(a.max_parts, a.num_kv_heads), dim3(kWaves * kWave), lds_b, stream,
+                         a);
     int st = check_launch("paged_decode_balanced_kernel");
     if (st) return st;
     hipLaunchKernelGGL((paged_decode_merge_balanced_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs),
@@ -826,14 +844,14 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = p->dtype == VAA_DTYPE_BF16;
   switch (p->head_size) {
-    case 32: return bf ? launch_decode<32, bf16>(a, sp.balanced, s)
-                       : launch_decode<32, f16>(a, sp.balanced, s);
-    case 64: return bf ? launch_decode<64, bf16>(a, sp.balanced, s)
-                       : launch_decode<64, f16>(a, sp.balanced, s);
-    case 96: return bf ? launch_decode<96, bf16>(a, sp.balanced, s)
-                       : launch_decode<96, f16>(a, sp.balanced, s);
-    case 128: return bf ? launch_decode<128, bf16>(a, sp.balanced, s)
-                        : launch_decode<128, f16>(a, sp.balanced, s);
+    case 32: return bf ? launch_decode<32, bf16>(a, sp.balanced, sp.shared, s)
+                       : launch_decode<32, f16>(a, sp.balanced, sp.shared, s);
+    case 64: return bf ? launch_decode<64, bf16>(a, sp.balanced, sp.shared, s)
+                       : launch_decode<64, f16>(a, sp.balanced, sp.shared, s);
+    case 96: return bf ? launch_decode<96, bf16>(a, sp.balanced, sp.shared, s)
+                       : launch_decode<96, f16>(a, sp.balanced, sp.shared, s);
+    case 128: return bf ? launch_decode<128, bf16>(a, sp.balanced, sp.shared, s)
+                        : launch_decode<128, f16>(a, sp.balanced, sp.shared, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
 }

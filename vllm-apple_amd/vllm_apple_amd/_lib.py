@@ -30,11 +30,12 @@ VAA_INDEX_I64 = 1
 
 # partition_size value asking decode to split by the actual lengths on the device.
 VAA_PARTITION_BALANCED = -1
+VAA_PARTITION_BALANCED_SHARED = -2
 
 # Element types of caches, queries, new K/V and outputs (vaa_attn_params.dtype).
 VAA_DTYPE_F16 = 0
 VAA_DTYPE_BF16 = 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class NativeLibraryError(RuntimeError):

@@ -287,7 +287,7 @@ class HipAttentionImpl(AttentionImpl):
                                        attn_metadata.slot_mapping[:n], layout="vllm")
             nd = attn_metadata.num_decode_tokens
 
-            def decode():
+            def decode(shared=False):
                 # Host lengths, only if already cached (never a device sync here).
                 lens_host = attn_metadata._seq_lens_cpu
                 kernels.paged_decode(query[:nd], key_cache, value_cache,
@@ -295,7 +295,8 @@ class HipAttentionImpl(AttentionImpl):
                                      attn_metadata.seq_lens[:nd], scale=self.scale,
                                      max_seq_len=attn_metadata.max_seq_len, layout="vllm",
                                      output=output[:nd],
-                                     seq_lens_host=lens_host[:nd] if lens_host else None)
+                                     seq_lens_host=lens_host[:nd] if lens_host else None,
+                                     shared=shared)
 
             def prefill():
                 kernels.paged_prefill(query[nd:n], key_cache, value_cache,
@@ -308,7 +309,7 @@ class HipAttentionImpl(AttentionImpl):
             if nd > 0 and n > nd and _overlap_enabled():
                 # Mixed step: prefill (MFMA) and decode (HBM) run concurrently;
                 # the results are bit-identical to running them in turn.
-                kernels.overlap(prefill, decode, query.device)
+                kernels.overlap(prefill, lambda: decode(shared=True), query.device)
             else:
                 if nd > 0:
                     decode()

@@ -284,6 +284,7 @@ _SHORT_START = 0.5
 _BALANCED_MIN_TOKENS = 512
 _BALANCED_MAX_SEQS = 8192
 PARTITION_BALANCED = _lib.VAA_PARTITION_BALANCED
+PARTITION_BALANCED_SHARED = _lib.VAA_PARTITION_BALANCED_SHARED
 _num_cus: dict[int, int] = {}
 
 
@@ -364,7 +365,7 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
                  max_seq_len: int, layout: str = "kernel", output: torch.Tensor | None = None,
                  new_keys: torch.Tensor | None = None, new_values: torch.Tensor | None = None,
                  partition_size: int = 0, workspace: torch.Tensor | None = None,
-                 seq_lens_host=None, stream=None) -> torch.Tensor:
+                 seq_lens_host=None, shared: bool = False, stream=None) -> torch.Tensor:
     """Paged GQA decode attention, one query token per sequence.
 
     query [num_seqs, H, D] fp16 or bf16 (the caches', new K/V's and output's
@@ -375,6 +376,9 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
     seq_lens_host (host copies of the lengths, no device sync needed) and
     partition_size 0 the split-K mode is chosen from the actual lengths;
     partition_size PARTITION_BALANCED splits by the lengths on the device.
+    shared=True says the launch runs concurrently with another kernel (see
+    overlap): an automatic balanced split then uses PARTITION_BALANCED_SHARED,
+    two half-size workgroups per CU that share CUs with the other kernel.
     """
     _require_gpu(query, key_cache, value_cache, block_table, seq_lens, output, new_keys, new_values)
     dt = _attn_dtype(query=query, key_cache=key_cache, value_cache=value_cache, output=output,
@@ -392,6 +396,8 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
     if partition_size == 0 and seq_lens_host is not None:
         kvh = key_cache.shape[1] if layout == "kernel" else key_cache.shape[2]
         partition_size = choose_partition_size(seq_lens_host, kvh, device_cus(query.device))
+        if shared and partition_size == PARTITION_BALANCED:
+            partition_size = PARTITION_BALANCED_SHARED
     p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
                     num_query_heads=query.shape[1], scale=scale, num_seqs=num_seqs,
                     max_seq_len=max_seq_len, max_blocks_per_seq=block_table.shape[1],
