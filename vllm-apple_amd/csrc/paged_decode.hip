@@ -563,10 +563,17 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
 
 // Second pass for split sequences:
 //   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p.
+// kMergeSplit thread groups of D threads each merge every kMergeSplit-th
+// partition (shorter dependent load chains for the long-context split); the
+// group states are then merged the same way through LDS.
+constexpr int kMergeSplit = 4;
+
 template <int D, typename T>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(D* kMergeSplit)
 paged_decode_merge_kernel(DecodeArgs a) {
-  const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+  __shared__ float st[kMergeSplit][3][D];
+  const int qh = blockIdx.x, seq = blockIdx.y;
+  const int d = threadIdx.x % D, grp = threadIdx.x / D;
   int L = a.seq_lens[seq];
   const int cap = a.max_blocks * a.block_size;
   if (L > cap) L = cap;
@@ -576,10 +583,18 @@ paged_decode_merge_kernel(DecodeArgs a) {
   if (n_parts <= 1) return;  // written directly by the decode kernel
   const int64_t row0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh) * a.max_parts;
   MergeAcc m;
-#pragma unroll 8
-  for (int p = 0; p < n_parts; ++p)
+#pragma unroll 4
+  for (int p = grp; p < n_parts; p += kMergeSplit)
     m.add(a.ws_ml[(row0 + p) * 2], a.ws_ml[(row0 + p) * 2 + 1], a.ws_acc[(row0 + p) * D + d]);
-  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(m.value());
+  st[grp][0][d] = m.M;
+  st[grp][1][d] = m.den;
+  st[grp][2][d] = m.num;
+  __syncthreads();
+  if (grp != 0) return;
+  MergeAcc t;
+#pragma unroll
+  for (int g = 0; g < kMergeSplit; ++g) t.add(st[g][0][d], st[g][1][d], st[g][2][d]);
+  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(t.value());
 }
 
 int g_num_cus = 0;
@@ -747,8 +762,8 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
   }
   int st = check_launch("paged_decode_kernel");
   if (st || a.max_parts <= 1) return st;
-  hipLaunchKernelGGL((paged_decode_merge_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs), dim3(D),
-                     0, stream, a);
+  hipLaunchKernelGGL((paged_decode_merge_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs),
+                     dim3(D * kMergeSplit), 0, stream, a);
   return check_launch("paged_decode_merge_kernel");
 }
 
