@@ -71,7 +71,7 @@ def test_kv_write_slots_bf16_bit_exact(gpu):
     assert np.array_equal(bits(vd).view(np.uint16), vr.view(np.uint16))
 
 
-@pytest.mark.parametrize("part", [0, 256, -1])
+@pytest.mark.parametrize("part", [0, 256, 2048, -1, -2])
 @pytest.mark.parametrize("layout", ["kernel", "vllm"])
 def test_decode_bf16_fused_write(gpu, part, layout):
     """C2 shape (32q/8kv, D128) in bf16: fused KV write bit-exact, output vs fp64."""
