@@ -19,11 +19,13 @@ def _bits(t: torch.Tensor) -> np.ndarray:
 def test_topk_random_rows(gpu, V, k, dtype):
     from vllm_apple_amd import kernels
 
-    if k > V:
-        pytest.skip("k > vocab")
     print(f"[case] topk V={V} k={k} {dtype}", flush=True)
     g = torch.Generator().manual_seed(V + k)
     logits = (torch.randn(9, V, generator=g) * 4).to(dtype)
+    if k > V:  # more than the vocabulary: refused before any launch
+        with pytest.raises(ValueError, match="must be in 1"):
+            kernels.topk_logits(logits.cuda(), k)
+        return
     idx, vals = kernels.topk_logits(logits.cuda(), k)
     torch.cuda.synchronize()
     ref_idx, ref_vals = otk.topk(_bits(logits), k)
