@@ -177,6 +177,23 @@ def _timed(fn, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def _timed_eager(fn, steps: int) -> float:
+    """Average time (ms) of `steps` eager calls of fn between two events on
+    the launch stream (host-side launch cost included, as a caller sees it)."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def _timed_rot(fns, steps: int, warmup: int) -> float:
     """_timed over a rotation: call i runs fns[i % len(fns)], each on its own
     copy of the data, so the bytes touched per rotation exceed the 256 MB
@@ -320,8 +337,8 @@ def wl_c5(args) -> dict:
                               output=out[nd:])
 
     def attn_step():
-        # As the backend runs a mixed step: the KV write, then prefill (side
-        # stream) and decode (current stream) concurrently.
+        # As the backend runs a mixed step: the KV write, then prefill (current
+        # stream) and decode (side stream, shared split) concurrently.
         kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache, b.slot_mapping)
         kernels.overlap(prefill, lambda: decode(shared=True), dev)
 
@@ -332,6 +349,9 @@ def wl_c5(args) -> dict:
 
     t_attn = _timed(attn_step, args.steps, args.warmup)
     t_attn_serial = _timed(attn_step_serial, args.steps, args.warmup)
+    # Eager calls too: vLLM runs the attention of mixed batches outside graphs.
+    t_attn_eager = _timed_eager(attn_step, args.steps)
+    t_attn_serial_eager = _timed_eager(attn_step_serial, args.steps)
     # Layer ops: each timed over a rotation of input/output copies whose bytes
     # exceed the 256 MB Infinity Cache.
     x, w = b.extra["hidden"], b.extra["norm_weight"]
@@ -411,6 +431,8 @@ def wl_c5(args) -> dict:
     rec = {"workload": "C5", "note": "56 decodes + 8 x 256-token chunks; layer ops over 2104 tokens",
            "attention_step_ms": round(t_attn, 5),
            "attention_step_serial_ms": round(t_attn_serial, 5),
+           "attention_step_eager_ms": round(t_attn_eager, 5),
+           "attention_step_serial_eager_ms": round(t_attn_serial_eager, 5),
            "attention_decode_kv_bytes": kv_read,
            "attention_prefill_flops": 4.0 * D * H * pre_ctx}
     rec["qkv_epilogue_three_pass_ms"] = round(t_three, 5)

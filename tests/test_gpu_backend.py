@@ -360,3 +360,42 @@ def test_forward_mixed_overlap_matches_serial_and_graph_replays(gpu, monkeypatch
         torch.cuda.synchronize()
         assert torch.equal(out, outs["1"][0]), f"replay {r}"
         _ = (out.float() * 2).sum().item()  # eager work between replays
+
+
+def test_forward_mixed_overlap_balanced_shared_split(gpu, monkeypatch):
+    """A mixed step whose decodes take the balanced split (host lengths known,
+    many ragged contexts): overlapped, decode runs the shared split beside the
+    prefill; the result matches the oracle and the serial step within the
+    attention tolerance (the two splits sum partials in a different order)."""
+    from vllm_apple_amd import backend as B
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    g = torch.Generator().manual_seed(12)
+    dec = torch.randint(300, 6000, (40,), generator=g).tolist()
+    b = _mixed_batch(seed=12, dec_lens=tuple(dec), pre=((2000, 128), (700, 96)))
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    scale = 1 / math.sqrt(D)
+    impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv = b["qkv"].to(dev)
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    from vllm_apple_amd import kernels
+
+    assert kernels.choose_partition_size(dec, KV, kernels.device_cus(dev)) == \
+        kernels.PARTITION_BALANCED
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv(B.OVERLAP_ENV, mode)
+        md = _metadata(b, dev)
+        md._seq_lens_cpu = b["lens"].tolist()
+        kv_cache = b["kv_cache"].to(dev)
+        out = torch.zeros((T, H, D), dtype=torch.float16, device=dev)
+        impl.forward(None, q, k, v, kv_cache, md, output=out)
+        torch.cuda.synchronize()
+        outs[mode] = host(out)
+    ref, _, _ = _oracle(b, scale)
+    assert_close(outs["1"], ref, what="overlapped mixed step (shared split)")
+    assert_close(outs["0"], ref, what="serial mixed step")
+    assert np.array_equal(outs["0"][len(dec):], outs["1"][len(dec):]), "prefill rows"

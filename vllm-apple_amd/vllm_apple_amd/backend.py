@@ -307,8 +307,9 @@ class HipAttentionImpl(AttentionImpl):
                 tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,
                                                      attn_metadata.seq_lens, n)
             if nd > 0 and n > nd and _overlap_enabled():
-                # Mixed step: prefill (MFMA) and decode (HBM) run concurrently;
-                # the results are bit-identical to running them in turn.
+                # Mixed step: prefill (MFMA-bound, current stream, dispatched
+                # first) and decode (HBM-bound, side stream, shared split) run
+                # concurrently.
                 kernels.overlap(prefill, lambda: decode(shared=True), query.device)
             else:
                 if nd > 0:

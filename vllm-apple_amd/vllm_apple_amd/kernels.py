@@ -234,16 +234,17 @@ def decode_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 _side_streams: dict[int, torch.cuda.Stream] = {}
 
 
-def overlap(side_fn, main_fn, device: torch.device | None = None) -> None:
-    """Run side_fn on a side stream and main_fn on the current stream at the
-    same time; both start after the work already on the current stream, and
-    the current stream waits for the side stream before returning (so callers,
-    the caching allocator and graph capture see one ordered step).  side_fn is
-    enqueued first.  Used for the prefill (MFMA-bound, side) and decode
-    (HBM-bound, current) halves of a mixed step: prefill workgroups take the
-    CUs first and decode workgroups fill them as the long-context prefill
-    tail drains (C5 attention step 800 -> 695 us on MI355X).  The side stream
-    keeps the default priority."""
+def overlap(first_fn, second_fn, device: torch.device | None = None) -> None:
+    """Run first_fn on the current stream and second_fn on a side stream at the
+    same time.  Both start after the work already on the current stream;
+    first_fn is enqueued first on the stream that is already running, so its
+    kernels dispatch first whether the step runs eagerly or from a captured
+    graph.  The current stream waits for the side stream before returning
+    (callers, the caching allocator and graph capture see one ordered step).
+    Used for the prefill (MFMA-bound, first) and decode (HBM-bound, second,
+    with the shared balanced split) halves of a mixed step: C5 attention step
+    about 0.80 -> 0.61 ms on MI355X, eager or replayed.  The side stream keeps
+    the default priority."""
     main = torch.cuda.current_stream(device)
     idx = main.device.index if main.device.index is not None else torch.cuda.current_device()
     side = _side_streams.get(idx)
@@ -251,9 +252,9 @@ def overlap(side_fn, main_fn, device: torch.device | None = None) -> None:
         side = torch.cuda.Stream(device=main.device)
         _side_streams[idx] = side
     side.wait_stream(main)
+    first_fn()
     with torch.cuda.stream(side):
-        side_fn()
-    main_fn()
+        second_fn()
     main.wait_stream(side)
 
 
