@@ -11,7 +11,11 @@
 //              head of the GQA group, so each K/V byte is read from HBM once.
 //   block    = 8 waves; each wave streams a contiguous run of 16-token tiles
 //              with its own (max, sum, acc) and the waves are combined in LDS
-//              at the end.
+//              at the end.  Fixed partitions of at most 1024 tokens and the
+//              shared balanced split (VAA_PARTITION_BALANCED_SHARED) use
+//              4-wave workgroups, two per CU: one's start-up overlaps the
+//              other's streaming, or a concurrent kernel's workgroup takes
+//              the other half of the CU.
 //   split-K  = only when the (seq, kv_head) pairs cannot fill the GPU or the
 //              lengths are unequal; partials (max, sum, acc) go to a workspace
 //              and a second kernel merges them (log-sum-exp).  The merge is a
