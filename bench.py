@@ -46,7 +46,8 @@ def parse() -> argparse.Namespace:
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="headline",
-                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C2bf16", "topk", "all"],
+                    choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C5mlp", "C2bf16", "topk",
+                             "all"],
                     help="headline = the contract line; the others print one JSON line per "
                          "BASELINE config (measurement record, not the driver's metric)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -457,6 +458,43 @@ def wl_c2bf16(args) -> dict:
     return _decode_record("C2-bf16", b, args, 0, "headline shape in bf16 (extension)")
 
 
+def wl_c5mlp(args) -> dict:
+    """C5's SwiGLU with its producer: the gated MLP's up projection
+    (2104 tokens, hidden 5120, intermediate 32768; x N(0,1), the fused
+    gate_up weight [65536, 5120] N(0, 1/5120)) with the SiLU*mul epilogue in
+    one MFMA kernel, against the reference's order on this GPU: the
+    projection as a library GEMM (torch.matmul, hipBLASLt) into a [T, 2I]
+    buffer, then vaa_silu_mul over its halves."""
+    import torch
+
+    from vllm_apple_amd import kernels
+
+    dev = torch.device("cuda:0")
+    T, H, I = 2104, 5120, 32768
+    g = torch.Generator(device=dev).manual_seed(55)
+    x = torch.randn(T, H, generator=g, device=dev).half()
+    w = (torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).half()
+    act = torch.empty(T, I, dtype=torch.float16, device=dev)
+    gu = torch.empty(T, 2 * I, dtype=torch.float16, device=dev)
+    t_fused = _timed(lambda: kernels.gate_up_silu(x, w, out=act), args.steps, args.warmup)
+    t_gemm = _timed(lambda: torch.matmul(x, w.T, out=gu), args.steps, args.warmup)
+
+    def unfused():
+        torch.matmul(x, w.T, out=gu)
+        kernels.silu_mul(gu[:, :I], gu[:, I:], out=act)
+
+    t_unfused = _timed(unfused, args.steps, args.warmup)
+    flops = 2.0 * T * H * 2 * I
+    tf = flops / (t_fused * 1e-3) / 1e12
+    return {"workload": "C5mlp", "note": "gate_up projection + SwiGLU, 2104 x 5120 -> 2 x 32768",
+            "flops": flops,
+            "gate_up_silu_ms": round(t_fused, 5), "gate_up_silu_tflops": round(tf, 1),
+            "pct_mfma_peak_f16": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 2),
+            "library_gemm_ms": round(t_gemm, 5),
+            "library_gemm_tflops": round(flops / (t_gemm * 1e-3) / 1e12, 1),
+            "library_gemm_plus_silu_mul_ms": round(t_unfused, 5)}
+
+
 def wl_topk(args) -> dict:
     """Top-k logits selection at the end of a step: k=50 (the reference's
     default) over a 128256-entry vocabulary (the 32q/8kv hd128 family's), for
@@ -488,7 +526,7 @@ def wl_topk(args) -> dict:
 
 
 WORKLOADS = {"C1": wl_c1, "C2u": wl_c2u, "C3": wl_c3, "C4": wl_c4, "C5": wl_c5,
-             "C2bf16": wl_c2bf16, "topk": wl_topk}
+             "C5mlp": wl_c5mlp, "C2bf16": wl_c2bf16, "topk": wl_topk}
 
 
 def main() -> int:
@@ -507,7 +545,7 @@ def main() -> int:
 
     _lib.load()
     if args.workload != "headline":
-        names = (["C1", "C2u", "C3", "C4", "C5", "C2bf16", "topk"] if args.workload == "all"
+        names = (["C1", "C2u", "C3", "C4", "C5", "C5mlp", "C2bf16", "topk"] if args.workload == "all"
                  else [args.workload])
         for name in names:
             print(json.dumps(WORKLOADS[name](args)), flush=True)

@@ -313,6 +313,28 @@ int vaa_silu_mul_2d(const uint16_t* gate, const uint16_t* up, uint16_t* output,
                     int64_t rows, int64_t cols, int64_t gate_stride,
                     int64_t up_stride, int64_t output_stride, int dtype, void* stream);
 
+/*
+ * Gated-MLP up projection with the SwiGLU epilogue, on the matrix cores:
+ *   output[t, i] = round16(silu(g) * u),
+ *   g = sum_h x[t, h] w_gate[i, h],   u = sum_h x[t, h] w_up[i, h],
+ * with g and u accumulated in fp32 and not rounded before the epilogue
+ * (silu and the product as vaa_silu_mul).  Replaces the reference's gated
+ * path of EngineMLP (vllm_apple/engine/ops/mlp.py:247-330): gate_proj and
+ * up_proj GEMMs into [T, I] intermediates (weights [I, H], transpose_B) and
+ * encode_silu_mul over them (elementwise.py:114-124); the fused gate_up_proj
+ * weight [2I, H] is passed as w_gate = w, w_up = w + I * w_stride.
+ * x: [num_tokens, hidden_size] at row stride x_stride; weights at row stride
+ * w_stride; output [num_tokens, intermediate_size] at row stride
+ * output_stride (strides in elements).  hidden_size must be a multiple of
+ * 64 and intermediate_size of 128 (VAA_ERR_UNSUPPORTED otherwise); x and
+ * the weights 16-byte aligned with strides that are multiples of 8, the
+ * output 8-byte aligned with a stride that is a multiple of 4.
+ */
+int vaa_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint16_t* w_gate,
+                     const uint16_t* w_up, int64_t w_stride, uint16_t* output,
+                     int64_t output_stride, int num_tokens, int hidden_size,
+                     int intermediate_size, int dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused QKV epilogue
  * ---------------------------------------------------------------------- */

@@ -8,13 +8,21 @@ rope_neox  vllm_apple/engine/ops/elementwise.py:185-239 with the cos/sin table
            (cos, sin)[positions[t], i], in fp64 from the fp32 table.
 cos_sin    the table itself, same numpy float32 construction.
 silu_mul   elementwise.py:114-124: g / (1 + exp(-g)) * u in fp64.
+gate_up_silu  the gated MLP's first half, vllm_apple/engine/ops/mlp.py:247-330:
+           gate = x W_gate^T and up = x W_up^T (transpose_B GEMMs, weights
+           [I, H]; a fused gate_up_proj [2I, H] holds the gate rows first,
+           :267-296), then silu_mul(gate, up); all in fp64 from the 16-bit
+           inputs, the intermediates not rounded.
 
 Pinning (tests/test_oracle_layer_ops.py): rms_norm against the reference
 test's own formula (tests/metal/test_transformer_block.py:136-199, seed 42,
 [4,128], eps 1e-6) and torch.nn.functional.rms_norm; rope_neox against the
 reference's torch formula (tests/unit/test_rope_equiv.py:42-66), pos 0 ->
 identity, per-pair norm preservation, and composition R(a)R(b) = R(a+b);
-silu_mul against torch.nn.functional.silu and its closed-form limits.
+silu_mul against torch.nn.functional.silu and its closed-form limits;
+gate_up_silu against numpy's matmul composed with the pinned silu_mul, one-hot
+activations (which select weight column h, so a transposed operand fails),
+zero gate or up weights, and the gate/up order of a fused weight.
 """
 from __future__ import annotations
 
@@ -62,3 +70,15 @@ def rope_neox(x: np.ndarray, positions: np.ndarray, cos: np.ndarray, sin: np.nda
 def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     gf = g.astype(np.float64)
     return gf / (1.0 + np.exp(-gf)) * u.astype(np.float64)
+
+
+def gate_up_silu(x: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray | None = None) -> np.ndarray:
+    """silu(x W_gate^T) * (x W_up^T) in fp64; with w_up None, w_gate is the
+    fused [2I, H] gate_up weight, gate rows first."""
+    if w_up is None:
+        half = w_gate.shape[0] // 2
+        w_gate, w_up = w_gate[:half], w_gate[half:]
+    xf = x.astype(np.float64)
+    g = np.einsum("th,ih->ti", xf, w_gate.astype(np.float64))
+    u = np.einsum("th,ih->ti", xf, w_up.astype(np.float64))
+    return silu_mul(g, u)

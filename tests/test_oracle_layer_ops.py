@@ -170,3 +170,37 @@ def test_planted_layer_op_mistakes_are_caught():
     # sign flip in the rotation
     r0 = x3[..., :32].astype(np.float64) * c + x3[..., 32:].astype(np.float64) * s
     assert not np.allclose(r0, _complex_rope(x3, pos, 1e4, 64)[..., :32], atol=1e-2)
+
+
+# -- gated MLP up projection + SwiGLU (mlp.py:247-330) ----------------------------------
+def test_gate_up_silu_vs_matmul_and_special_cases():
+    rs = np.random.RandomState(7)
+    T, H, I = 5, 96, 40
+    x = rs.randn(T, H).astype(np.float16)
+    wg = (rs.randn(I, H) / np.sqrt(H)).astype(np.float16)
+    wu = (rs.randn(I, H) / np.sqrt(H)).astype(np.float16)
+    # numpy's matmul composed with the pinned silu_mul
+    g = np.matmul(x.astype(np.float64), wg.astype(np.float64).T)
+    u = np.matmul(x.astype(np.float64), wu.astype(np.float64).T)
+    got = olo.gate_up_silu(x, wg, wu)
+    np.testing.assert_allclose(got, olo.silu_mul(g, u), rtol=1e-12, atol=1e-14)
+    # one-hot activations select weight column h of both matrices
+    eye = np.zeros((3, H), dtype=np.float16)
+    hs = [0, 17, H - 1]
+    for t, h in enumerate(hs):
+        eye[t, h] = 1.0
+    sel = olo.gate_up_silu(eye, wg, wu)
+    for t, h in enumerate(hs):
+        np.testing.assert_allclose(sel[t], olo.silu_mul(wg[:, h], wu[:, h]), rtol=1e-12)
+    # a zero gate (silu(0) = 0) or a zero up projection gives zero
+    assert not olo.gate_up_silu(x, np.zeros_like(wg), wu).any()
+    assert not olo.gate_up_silu(x, wg, np.zeros_like(wu)).any()
+    # fused [2I, H] weight: gate rows first
+    fused = np.concatenate([wg, wu])
+    np.testing.assert_array_equal(olo.gate_up_silu(x, fused), got)
+    # planted: halves swapped (silu on the up projection) or a transposed product
+    assert not np.allclose(olo.gate_up_silu(x, wu, wg), got, rtol=1e-3)
+    sq = rs.randn(H, H).astype(np.float16)
+    xs = rs.randn(2, H).astype(np.float16)
+    assert not np.allclose(olo.gate_up_silu(xs, sq, sq.T.copy()),
+                           olo.gate_up_silu(xs, sq, sq), rtol=1e-3)

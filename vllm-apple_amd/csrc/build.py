@@ -31,6 +31,7 @@ SOURCES = [
     "index_ops.hip",
     "qkv_epilogue.hip",
     "topk.hip",
+    "gate_up_silu.hip",
 ]
 
 ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")

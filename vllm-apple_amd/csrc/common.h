@@ -57,6 +57,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// silu(g) * u in fp32: g / (1 + 2^(-g log2 e)) with the hardware exp and
+// reciprocal, shared by the SwiGLU pass and the gate/up GEMM epilogue so the
+// two round alike.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+  const float e = fast_exp2(-g * kLog2e);
+  return (g * __builtin_amdgcn_rcpf(1.f + e)) * u;
+}
+
 // ------------------------------------------------- 16-bit element types --
 // The attention kernels keep K/V/Q/outputs as raw 16-bit storage and are
 // templated on the element type only where values are converted or fed to

@@ -1,0 +1,284 @@
+// Gated-MLP up projection with the SwiGLU epilogue, on the matrix cores:
+//
+//   out[t, i] = round16(silu(g) * u),  g = x[t, :] . w_gate[i, :],  u = x[t, :] . w_up[i, :]
+//
+// with g and u accumulated in fp32 and never rounded to 16 bits.  The
+// reference runs this as two GEMMs into [T, I] gate and up buffers followed by
+// a silu_mul pass over both (vllm_apple/engine/ops/mlp.py:247-330 with
+// elementwise.py:114-124); here the epilogue reads g and u from the
+// accumulators, so neither intermediate is written or read back.
+//
+// Tiling (one 4-wave workgroup per CU, 128 KB of LDS):
+//   workgroup = 256 tokens x 128 output columns: a 256 x 256 product of the
+//               token rows of x against 256 weight rows (128 gate, then the
+//               128 up rows of the same columns);
+//   wave w    = tokens 128*(w/2) .. +128 x columns 64*(w%2) .. +64, a 4 x 4
+//               grid of 32x32 MFMA tiles (two gate and two up row blocks by
+//               four token blocks), so the gate and up values of one output
+//               sit in the same lane, in the same accumulator position;
+//   k-step    = 64 hidden elements.  The product is computed transposed,
+//               W x^T, with v_mfma_f32_32x32x16: the A operand is 8 weights of
+//               one row and the B operand 8 activations of one token, both
+//               read from LDS with ds_read_b128.  Lanes 0-31 take the first
+//               half of the step's 64 elements and lanes 32-63 the second
+//               (the contraction index is a sum, so any assignment that the
+//               two operands share is exact).
+//
+// Memory: both operands are rows contiguous in the hidden dimension.  They
+// move from HBM to LDS with direct loads (buffer_load_dwordx4 ... lds: lane i
+// of a wave writes LDS bytes [16i, 16i + 16) after the wave-uniform base in
+// M0), double-buffered in four distinct LDS arrays, so the next k-step
+// streams in during this step's MFMAs.  The 16-byte chunks of each 128-byte
+// LDS row are XOR-swizzled by row & 7, so the eight consecutive rows that an
+// operand read spans per 128 bytes hit distinct banks.  Token rows past
+// num_tokens read the last token's row (always in bounds) and their outputs
+// are not stored.
+//
+// Workgroup order: the 8 XCDs each take a contiguous range of (column tile,
+// token tile) pairs, token tile fastest, so all the token tiles that share a
+// weight tile run at the same time on one XCD and read it through its L2.
+#include "common.h"
+
+namespace vaa {
+namespace {
+
+constexpr int kGT = 256;                         // tokens per workgroup
+constexpr int kGI = 128;                         // output columns per workgroup
+constexpr int kGK = 64;                          // hidden elements per k-step
+constexpr int kGWaves = 4;
+constexpr int kGThreads = kGWaves * kWave;
+constexpr int kGRowB = kGK * 2;                  // bytes per LDS row
+constexpr int kGTileB = 256 * kGRowB;            // one operand tile: 256 rows, 32 KB
+constexpr int kGLoads = kGTileB / (kGThreads * 16);  // direct loads per wave per operand
+constexpr int kGXcds = 8;
+static_assert(kGLoads == 8, "eight 1 KB direct loads per wave and operand");
+
+// Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
+// no swizzle, offsets checked against the byte range in word 2.
+constexpr int kBufDword3 = 0x00020000;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+struct GluArgs {
+  const char* x;
+  const char* wg;
+  const char* wu;
+  char* out;
+  int64_t xs, ws, os;  // row strides, bytes
+  int num_tokens, ksteps, t_tiles, tiles;
+};
+
+// s_waitcnt vmcnt(0) lgkmcnt(0): every direct load and LDS access of this
+// wave has landed.
+__device__ __forceinline__ void glu_wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+
+template <typename T>
+__global__ void __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gate_up_silu_kernel(GluArgs a) {
+  __shared__ __align__(16) char w0[kGTileB];
+  __shared__ __align__(16) char w1[kGTileB];
+  __shared__ __align__(16) char x0[kGTileB];
+  __shared__ __align__(16) char x1[kGTileB];
+
+  const int per_xcd = static_cast<int>(gridDim.x) / kGXcds;
+  const int logical = (static_cast<int>(blockIdx.x) % kGXcds) * per_xcd +
+                      static_cast<int>(blockIdx.x) / kGXcds;
+  if (logical >= a.tiles) return;
+  const int t0 = (logical % a.t_tiles) * kGT;
+  const int i0 = (logical / a.t_tiles) * kGI;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+
+  // Direct-load sources, as buffer loads: a wave-uniform resource and k
+  // offset, and a per-lane 32-bit offset.  Slot P of a tile is LDS row P / 8,
+  // physical chunk P % 8, which holds logical chunk (P % 8) ^ (row & 7).
+  // Weight rows 0-127 (waves 0 and 1) are the gate rows i0.., rows 128-255
+  // (waves 2 and 3) the up rows of the same columns, so each wave reads one
+  // weight matrix; its load q is 8 rows further on.  Every access stays
+  // inside its resource's range (rows of x are clamped to num_tokens - 1).
+  const char* wbase = (wave < 2 ? a.wg : a.wu) + static_cast<int64_t>(i0) * a.ws;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(wbase), 0, static_cast<int>(kGI * a.ws), kBufDword3);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(a.x), 0, static_cast<int>(a.num_tokens * a.xs), kBufDword3);
+  const int rw = 8 * (wave & 1) * kGLoads + (lane >> 3);  // weight row of load 0, mod 128
+  const int lc = (lane & 7) ^ (rw & 7);                    // a wave's rows agree mod 8
+  const int woff = rw * static_cast<int>(a.ws) + lc * 16;
+  const int wstep = 8 * static_cast<int>(a.ws);
+  int xoff[kGLoads];
+#pragma unroll
+  for (int q = 0; q < kGLoads; ++q) {
+    const int R = 8 * (wave * kGLoads + q) + (lane >> 3);
+    xoff[q] = min(t0 + R, a.num_tokens - 1) * static_cast<int>(a.xs) + lc * 16;
+  }
+  const int dst0 = 1024 * wave * kGLoads;
+
+  // Operand reads: row l % 32 of a 32-row block, logical chunk 4 (l / 32) + s.
+  const int l32 = lane & 31, hb = lane >> 5;
+  int rd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) rd[s] = l32 * kGRowB + (((4 * hb + s) ^ (l32 & 7)) << 4);
+  const int wi = wave & 1, wt = wave >> 1;
+  // Weight row blocks: gate 64wi, 64wi + 32; up 128 + 64wi, 128 + 64wi + 32.
+  const int wrow[4] = {64 * wi, 64 * wi + 32, kGI + 64 * wi, kGI + 64 * wi + 32};
+  const int xrow0 = 128 * wt;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[f][c][r] = 0.f;
+
+  auto fetch = [&](int ks, char* wd, char* xd) {
+    const int kb = ks * kGRowB;
+#pragma unroll
+    for (int q = 0; q < kGLoads; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void_t*)(wd + dst0 + 1024 * q), 16,
+                                               woff, kb + q * wstep, 0, 0);
+#pragma unroll
+    for (int q = 0; q < kGLoads; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void_t*)(xd + dst0 + 1024 * q), 16,
+                                               xoff[q], kb, 0, 0);
+  };
+  // Operand fragments of sub-step s (16 hidden elements per MFMA).
+  auto frags = [&](const char* wt_, const char* xt_, int s, u32x4 (&A)[4], u32x4 (&B)[4]) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+      A[f] = *reinterpret_cast<const u32x4*>(wt_ + wrow[f] * kGRowB + rd[s]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      B[c] = *reinterpret_cast<const u32x4*>(xt_ + (xrow0 + 32 * c) * kGRowB + rd[s]);
+  };
+  auto mfmas = [&](const u32x4 (&A)[4], const u32x4 (&B)[4]) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[f][c] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, A[f]),
+                                          __builtin_bit_cast(typename Elem<T>::x8, B[c]),
+                                          acc[f][c]);
+  };
+  // The four sub-steps of a k-step, with the next sub-step's operands read
+  // from LDS while this one's 16 MFMAs run (scheduling fences keep the reads
+  // ahead of the MFMAs they overlap).
+  auto math = [&](const char* wt_, const char* xt_) {
+    u32x4 A0[4], B0[4], A1[4], B1[4];
+    frags(wt_, xt_, 0, A0, B0);
+    frags(wt_, xt_, 1, A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(A0, B0);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(wt_, xt_, 2, A0, B0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(wt_, xt_, 3, A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(A0, B0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(A1, B1);
+  };
+  // One k-step on the current buffers: wait for their loads (this wave's,
+  // then everyone's through the barrier, which also retires the reads of the
+  // other buffers from the step before), start the next step's loads into the
+  // other buffers, then multiply.
+  auto step = [&](int ks, const char* cw, const char* cx, char* nw, char* nx) {
+    glu_wait_all();
+    __syncthreads();
+    if (ks + 1 < a.ksteps) fetch(ks + 1, nw, nx);
+    __builtin_amdgcn_sched_barrier(0);
+    math(cw, cx);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  fetch(0, w0, x0);
+  int ks = 0;
+  for (; ks + 2 <= a.ksteps; ks += 2) {
+    step(ks, w0, x0, w1, x1);
+    step(ks + 1, w1, x1, w0, x0);
+  }
+  if (ks < a.ksteps) step(ks, w0, x0, w1, x1);
+
+  // Epilogue.  The lane holds token xrow0 + 32c + l32 and, for row block f,
+  // columns 8 (r / 4) + 4 hb + r % 4 of that block: four runs of four
+  // consecutive columns, stored as 8-byte pieces.
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int tok = t0 + xrow0 + 32 * c + l32;
+    if (tok >= a.num_tokens) continue;
+    char* orow = a.out + static_cast<int64_t>(tok) * a.os;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int col = i0 + 64 * wi + 32 * j + 8 * g4 + 4 * hb;
+        T v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = Elem<T>::from_f(silu_mul1(acc[j][c][4 * g4 + e], acc[2 + j][c][4 * g4 + e]));
+        *reinterpret_cast<u32x2*>(orow + 2 * col) = __builtin_bit_cast(u32x2, v);
+      }
+  }
+}
+
+template <typename T>
+int launch_gate_up_silu(const GluArgs& a0, hipStream_t stream) {
+  GluArgs a = a0;
+  const int grid = (a.tiles + kGXcds - 1) / kGXcds * kGXcds;
+  hipLaunchKernelGGL((gate_up_silu_kernel<T>), dim3(grid), dim3(kGThreads), 0, stream, a);
+  return check_launch("gate_up_silu_kernel");
+}
+
+}  // namespace
+}  // namespace vaa
+
+using namespace vaa;
+
+extern "C" int vaa_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint16_t* w_gate,
+                                const uint16_t* w_up, int64_t w_stride, uint16_t* output,
+                                int64_t output_stride, int num_tokens, int hidden_size,
+                                int intermediate_size, int dtype, void* stream) {
+  const char* what = "vaa_gate_up_silu";
+  if (!valid_dtype(dtype)) return fail(VAA_ERR_UNSUPPORTED, "%s: dtype=%d", what, dtype);
+  if (num_tokens < 0 || hidden_size <= 0 || intermediate_size <= 0)
+    return fail(VAA_ERR_INVALID_ARG, "%s: num_tokens=%d hidden_size=%d intermediate_size=%d",
+                what, num_tokens, hidden_size, intermediate_size);
+  if (hidden_size % kGK != 0 || intermediate_size % kGI != 0)
+    return fail(VAA_ERR_UNSUPPORTED,
+                "%s: hidden_size=%d must be a multiple of %d and intermediate_size=%d of %d",
+                what, hidden_size, kGK, intermediate_size, kGI);
+  if (num_tokens == 0) return VAA_OK;
+  if (!x || !w_gate || !w_up || !output) return fail(VAA_ERR_INVALID_ARG, "%s: null pointer", what);
+  if (x_stride < hidden_size || w_stride < hidden_size || output_stride < intermediate_size ||
+      x_stride % 8 != 0 || w_stride % 8 != 0 || output_stride % 4 != 0)
+    return fail(VAA_ERR_INVALID_ARG,
+                "%s: strides x=%lld w=%lld out=%lld (x, w: multiples of 8 >= hidden_size; out: "
+                "a multiple of 4 >= intermediate_size)",
+                what, (long long)x_stride, (long long)w_stride, (long long)output_stride);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) ||
+      (reinterpret_cast<uintptr_t>(output) & 7u) != 0)
+    return fail(VAA_ERR_INVALID_ARG, "%s: x and weights must be 16-byte, output 8-byte aligned",
+                what);
+  GluArgs a;
+  a.x = reinterpret_cast<const char*>(x);
+  a.wg = reinterpret_cast<const char*>(w_gate);
+  a.wu = reinterpret_cast<const char*>(w_up);
+  a.out = reinterpret_cast<char*>(output);
+  a.xs = 2 * x_stride;
+  a.ws = 2 * w_stride;
+  a.os = 2 * output_stride;
+  a.num_tokens = num_tokens;
+  a.ksteps = hidden_size / kGK;
+  a.t_tiles = (num_tokens + kGT - 1) / kGT;
+  const int64_t tiles = static_cast<int64_t>(a.t_tiles) * (intermediate_size / kGI);
+  // Load offsets and buffer ranges are 31-bit: activation rows from x,
+  // weight rows from the workgroup's first row.
+  if (tiles > (1 << 30) || static_cast<int64_t>(num_tokens) * a.xs >= (int64_t(1) << 31) ||
+      static_cast<int64_t>(kGI) * a.ws >= (int64_t(1) << 31))
+    return fail(VAA_ERR_UNSUPPORTED, "%s: problem too large", what);
+  a.tiles = static_cast<int>(tiles);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == VAA_DTYPE_F16 ? launch_gate_up_silu<f16>(a, s) : launch_gate_up_silu<bf16>(a, s);
+}

@@ -223,11 +223,6 @@ __global__ void __launch_bounds__(256) rope_neox_scalar_kernel(RopeArgs<T> a) {
 
 // ----------------------------------------------------------------- SwiGLU --
 // elementwise.py:114-124: out = half(g / (1 + exp(-g)) * u) in fp32.
-__device__ __forceinline__ float silu_mul1(float g, float u) {
-  const float e = fast_exp2(-g * kLog2e);
-  return (g * __builtin_amdgcn_rcpf(1.f + e)) * u;
-}
-
 template <typename T>
 __global__ void __launch_bounds__(256)
 silu_mul_vec_kernel(const T* gate, const T* up, T* out, int64_t rows,

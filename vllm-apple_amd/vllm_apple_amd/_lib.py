@@ -101,6 +101,7 @@ SIGNATURES = {
     "vaa_rope_neox": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64, _I, _I, _P]),
     "vaa_silu_mul": (_I, [_P, _P, _P, _I64, _I, _P]),
     "vaa_silu_mul_2d": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P]),
+    "vaa_gate_up_silu": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "vaa_topk_workspace_size": (_I, [_I, _I, _I, _P]),
     "vaa_topk_logits": (_I, [_P, _I, _I, _I64, _I, _P, _P, _I64, _P, ctypes.c_size_t, _P]),
     "vaa_qkv_epilogue": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _I,

@@ -717,5 +717,44 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = No
     return out
 
 
+def gate_up_silu(x: torch.Tensor, gate_weight: torch.Tensor,
+                 up_weight: torch.Tensor | None = None, *, out: torch.Tensor | None = None,
+                 stream=None) -> torch.Tensor:
+    """SwiGLU of the gated-MLP up projection in one MFMA pass:
+    out = round16(silu(x @ gate_weight.T) * (x @ up_weight.T)), both products
+    accumulated in fp32 and never rounded before the epilogue.
+
+    x is [T, H] with contiguous rows.  The weights are [I, H] (vLLM's
+    gate_proj / up_proj layout, the reference's transpose_B GEMMs in
+    engine/ops/mlp.py:300-330), or, with up_weight None, gate_weight is the
+    fused gate_up_proj [2I, H] (gate rows first, mlp.py:267-296).  H must be a
+    multiple of 64 and I of 128.  fp16 or bf16."""
+    _require_gpu(x, gate_weight, up_weight, out)
+    if up_weight is None:
+        if gate_weight.dim() != 2 or gate_weight.shape[0] % 2:
+            raise ValueError("a fused gate_up weight must be [2I, H]")
+        i2 = gate_weight.shape[0] // 2
+        gate_weight, up_weight = gate_weight[:i2], gate_weight[i2:]
+    dt = _layer_dtype(x=x, gate_weight=gate_weight, up_weight=up_weight, out=out)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be [num_tokens, hidden] with contiguous rows")
+    t, h = x.shape
+    if (gate_weight.dim() != 2 or gate_weight.shape != up_weight.shape
+            or gate_weight.shape[1] != h):
+        raise ValueError("gate and up weights must both be [I, H] with x's H")
+    if (gate_weight.stride(1) != 1 or up_weight.stride(1) != 1
+            or gate_weight.stride(0) != up_weight.stride(0)):
+        raise ValueError("gate and up weights need contiguous rows at one row stride")
+    inter = gate_weight.shape[0]
+    if out is None:
+        out = torch.empty((t, inter), dtype=x.dtype, device=x.device)
+    if out.shape != (t, inter) or out.stride(1) != 1:
+        raise ValueError("out must be [num_tokens, intermediate] with contiguous rows")
+    _lib.call("vaa_gate_up_silu", x.data_ptr(), x.stride(0), gate_weight.data_ptr(),
+              up_weight.data_ptr(), gate_weight.stride(0), out.data_ptr(), out.stride(0), t, h,
+              inter, dt, _lib.stream_handle(stream))
+    return out
+
+
 def default_scale(head_size: int) -> float:
     return 1.0 / math.sqrt(head_size)
