@@ -2,7 +2,8 @@
 against the oracle (fp64 products, silu_mul of the unrounded values) within
 the north-star tolerance, and against the reference's unfused order (two
 GEMMs rounded to 16 bits, then silu_mul) within the rounding that the fusion
-removes.  Covers one and odd numbers of k-steps, token counts that leave a
+removes.  Covers 1, 2, 3, 5 and 7 k-steps (odd counts
+end on the first of the two LDS buffers), token counts that leave a
 partial token tile, fused and separate weights, strided rows and the C5 shape.
 """
 import numpy as np
@@ -23,8 +24,9 @@ def _inputs(T, H, I, dtype, seed):
     return x, w
 
 
-@pytest.mark.parametrize("T,H,I", [(1, 64, 128), (37, 192, 256), (256, 320, 128),
-                                   (300, 512, 384), (513, 128, 256), (1000, 1024, 512)])
+@pytest.mark.parametrize("T,H,I", [(1, 64, 128), (3, 128, 128), (37, 192, 256), (5, 320, 128),
+                                   (256, 320, 128), (300, 512, 384), (513, 448, 256),
+                                   (1000, 1024, 512)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gate_up_silu_vs_oracle(gpu, T, H, I, dtype):
     from vllm_apple_amd import kernels

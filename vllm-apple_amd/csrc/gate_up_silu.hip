@@ -28,11 +28,14 @@
 // move from HBM to LDS with direct loads (buffer_load_dwordx4 ... lds: lane i
 // of a wave writes LDS bytes [16i, 16i + 16) after the wave-uniform base in
 // M0), double-buffered in four distinct LDS arrays, so the next k-step
-// streams in during this step's MFMAs.  The 16-byte chunks of each 128-byte
-// LDS row are XOR-swizzled by row & 7, so the eight consecutive rows that an
-// operand read spans per 128 bytes hit distinct banks.  Token rows past
-// num_tokens read the last token's row (always in bounds) and their outputs
-// are not stored.
+// streams in during this step's MFMAs; its 16 loads per wave are spread one
+// after every second MFMA of the step's first half.  Each wave also touches
+// the weight rows of the step kPfDist ahead with one 4-byte load per row,
+// which pulls them from HBM into L2 before the direct loads ask for them.
+// The 16-byte chunks of each 128-byte LDS row are XOR-swizzled by row & 7,
+// so the eight consecutive rows that an operand read spans per 128 bytes hit
+// distinct banks.  Token rows past num_tokens read the last token's row
+// (always in bounds) and their outputs are not stored.
 //
 // Workgroup order: the 8 XCDs each take a contiguous range of (column tile,
 // token tile) pairs, token tile fastest, so all the token tiles that share a
@@ -68,9 +71,12 @@ struct GluArgs {
   int num_tokens, ksteps, t_tiles, tiles;
 };
 
-// s_waitcnt vmcnt(0) lgkmcnt(0): every direct load and LDS access of this
-// wave has landed.
-__device__ __forceinline__ void glu_wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+// s_waitcnt vmcnt(1) lgkmcnt(0), at the top of a k-step: every vector memory
+// load of this wave but the newest has landed.  Each step issues its 16
+// direct loads and then one L2 prefetch, and loads complete in issue order,
+// so the step's tiles are in LDS (as far as this wave's loads go; the barrier
+// that follows covers the other waves').
+__device__ __forceinline__ void glu_wait_tiles() { __builtin_amdgcn_s_waitcnt(0x0071); }
 
 template <typename T>
 __global__ void __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -131,16 +137,15 @@ gate_up_silu_kernel(GluArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[f][c][r] = 0.f;
 
-  auto fetch = [&](int ks, char* wd, char* xd) {
-    const int kb = ks * kGRowB;
-#pragma unroll
-    for (int q = 0; q < kGLoads; ++q)
+  // Direct load q (0-7 weights, 8-15 activations) of the k-step at byte
+  // offset kb into the tiles wd, xd.
+  auto load1 = [&](int q, int kb, char* wd, char* xd) {
+    if (q < kGLoads)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void_t*)(wd + dst0 + 1024 * q), 16,
                                                woff, kb + q * wstep, 0, 0);
-#pragma unroll
-    for (int q = 0; q < kGLoads; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void_t*)(xd + dst0 + 1024 * q), 16,
-                                               xoff[q], kb, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (lds_void_t*)(xd + dst0 + 1024 * (q - kGLoads)), 16, xoff[q - kGLoads], kb, 0, 0);
   };
   // Operand fragments of sub-step s (16 hidden elements per MFMA).
   auto frags = [&](const char* wt_, const char* xt_, int s, u32x4 (&A)[4], u32x4 (&B)[4]) {
@@ -151,55 +156,73 @@ gate_up_silu_kernel(GluArgs a) {
     for (int c = 0; c < 4; ++c)
       B[c] = *reinterpret_cast<const u32x4*>(xt_ + (xrow0 + 32 * c) * kGRowB + rd[s]);
   };
-  auto mfmas = [&](const u32x4 (&A)[4], const u32x4 (&B)[4]) {
+  // The 16 MFMAs of one sub-step; with ld, direct loads q0 .. q0 + 7, one
+  // after every second MFMA (scheduling fences keep that order).
+  auto mfmas = [&](const u32x4 (&A)[4], const u32x4 (&B)[4], bool ld, int q0, int kb,
+                   char* wd, char* xd) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        acc[f][c] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, A[f]),
-                                          __builtin_bit_cast(typename Elem<T>::x8, B[c]),
-                                          acc[f][c]);
+    for (int idx = 0; idx < 16; ++idx) {
+      const int f = idx >> 2, c = idx & 3;
+      acc[f][c] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, A[f]),
+                                        __builtin_bit_cast(typename Elem<T>::x8, B[c]),
+                                        acc[f][c]);
+      if (ld && (idx & 1)) load1(q0 + (idx >> 1), kb, wd, xd);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  // The four sub-steps of a k-step, with the next sub-step's operands read
-  // from LDS while this one's 16 MFMAs run (scheduling fences keep the reads
-  // ahead of the MFMAs they overlap).
-  auto math = [&](const char* wt_, const char* xt_) {
-    u32x4 A0[4], B0[4], A1[4], B1[4];
-    frags(wt_, xt_, 0, A0, B0);
-    frags(wt_, xt_, 1, A1, B1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(A0, B0);
-    __builtin_amdgcn_sched_barrier(0);
-    frags(wt_, xt_, 2, A0, B0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(A1, B1);
-    __builtin_amdgcn_sched_barrier(0);
-    frags(wt_, xt_, 3, A1, B1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(A0, B0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(A1, B1);
+  // L2 prefetch of the weight rows kPfDist steps ahead: one 4-byte load per
+  // row (one 128-byte line per row and step) of the wave's 64.  The values
+  // are summed into `sink` two steps later, when the wait at the top of the
+  // step has already covered them, and `sink` is kept alive by a store that
+  // never happens, so the loads are not dropped.
+  constexpr int kPfDist = 3;
+  const int pfw = (64 * (wave & 1) + lane) * static_cast<int>(a.ws);
+  uint32_t sink = 0, pfa = 0, pfb = 0;
+  auto prefetch = [&](int ks, uint32_t& slot) {
+    sink += slot;
+    slot = __builtin_amdgcn_raw_buffer_load_b32(wrs, pfw, min(ks + kPfDist, a.ksteps - 1) * kGRowB,
+                                                0);
   };
-  // One k-step on the current buffers: wait for their loads (this wave's,
-  // then everyone's through the barrier, which also retires the reads of the
-  // other buffers from the step before), start the next step's loads into the
-  // other buffers, then multiply.
-  auto step = [&](int ks, const char* cw, const char* cx, char* nw, char* nx) {
-    glu_wait_all();
+  // Step ks on the tiles (cw, cx): wait for them (this wave's loads, then
+  // everyone's through the barrier, which also retires every read of the
+  // other tiles in step ks - 1), then the four sub-steps with the next
+  // sub-step's operands read while this one's MFMAs run, and step ks + 1's
+  // loads (clamped to the last step: past the end they refill tiles that are
+  // not read again) into (nw, nx) among the first 32 MFMAs.
+  auto step = [&](int ks, const char* cw, const char* cx, char* nw, char* nx, uint32_t& slot) {
+    glu_wait_tiles();
     __syncthreads();
-    if (ks + 1 < a.ksteps) fetch(ks + 1, nw, nx);
+    const int kb = min(ks + 1, a.ksteps - 1) * kGRowB;
+    u32x4 A0[4], B0[4], A1[4], B1[4];
+    frags(cw, cx, 0, A0, B0);
+    frags(cw, cx, 1, A1, B1);
     __builtin_amdgcn_sched_barrier(0);
-    math(cw, cx);
+    mfmas(A0, B0, true, 0, kb, nw, nx);
+    frags(cw, cx, 2, A0, B0);
     __builtin_amdgcn_sched_barrier(0);
+    mfmas(A1, B1, true, 8, kb, nw, nx);
+    prefetch(ks, slot);
+    frags(cw, cx, 3, A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(A0, B0, false, 0, kb, nw, nx);
+    mfmas(A1, B1, false, 0, kb, nw, nx);
   };
 
-  fetch(0, w0, x0);
+  // Step 0's loads, then one prefetch so that the wait count holds from the
+  // first step.
+#pragma unroll
+  for (int q = 0; q < 2 * kGLoads; ++q) load1(q, 0, w0, x0);
+  prefetch(-1, pfb);
   int ks = 0;
   for (; ks + 2 <= a.ksteps; ks += 2) {
-    step(ks, w0, x0, w1, x1);
-    step(ks + 1, w1, x1, w0, x0);
+    step(ks, w0, x0, w1, x1, pfa);
+    step(ks + 1, w1, x1, w0, x0, pfb);
   }
-  if (ks < a.ksteps) step(ks, w0, x0, w1, x1);
+  if (ks < a.ksteps) step(ks, w0, x0, w1, x1, pfa);
+  // Every load has landed before the workgroup ends and its LDS is released.
+  __builtin_amdgcn_s_waitcnt(0x0070);
+  sink += pfa + pfb;
+  if (sink == 0x7f7f7f7fu && a.num_tokens < 0) a.out[0] = 0;
 
   // Epilogue.  The lane holds token xrow0 + 32c + l32 and, for row block f,
   // columns 8 (r / 4) + 4 hb + r % 4 of that block: four runs of four
