@@ -119,3 +119,61 @@ def test_gate_up_silu_c5_shape(gpu):
     wh = host(w)
     ref = olo.gate_up_silu(xs, wh[cols], wh[I + cols])
     assert_close(o[np.ix_(rows, cols)], ref, what="C5 rows x cols")
+
+
+def test_gate_up_silu_graph_replays_match_eager(gpu):
+    """Captured in a HIP graph and replayed three times, with eager work and
+    synchronizations between the replays: every replay equals the eager
+    result bit for bit."""
+    from vllm_apple_amd import kernels
+
+    print("[case] gate_up_silu graph replays", flush=True)
+    T, H, I = 300, 512, 384
+    x, w = _inputs(T, H, I, torch.float16, 21)
+    xd, wd = x.cuda(), w.cuda()
+    eager = kernels.gate_up_silu(xd, wd)
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kernels.gate_up_silu(xd, wd, out=out)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kernels.gate_up_silu(xd, wd, out=out)
+    for r in range(3):
+        out.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {r}"
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_engine_mlp_encode(gpu, fused):
+    """EngineMLP.encode (mlp.py:170-245): down_proj(silu(gate(x)) * up(x)) on
+    (buffer, byte offset) views inside an ENCODE phase, against the oracle's
+    activation rounded to fp16 and an fp64 down projection."""
+    from vllm_apple_amd.engine import EngineMLP, EngineStepContext
+
+    print(f"[case] EngineMLP fused={fused}", flush=True)
+    T, H, I = 37, 256, 512
+    x, w = _inputs(T, H, I, torch.float16, 8)
+    g = torch.Generator().manual_seed(9)
+    down = (torch.randn(H, I, generator=g) / I ** 0.5).half()
+    mlp = EngineMLP(None, H, I)
+    if fused:
+        mlp.set_weights(gate_up_proj=w.cuda(), down_proj=down.cuda())
+    else:
+        mlp.set_weights(gate_proj=w[:I].contiguous().cuda(), up_proj=w[I:].contiguous().cuda(),
+                        down_proj=down.cuda())
+    buf = torch.zeros(2 * T * H + 64, dtype=torch.float16, device="cuda")
+    buf[64:64 + T * H] = x.cuda().reshape(-1)
+    with EngineStepContext() as ctx:
+        mlp.encode(ctx, (buf, 128), (buf, 128 + 2 * T * H), T)
+    torch.cuda.synchronize()
+    out = host(buf[64 + T * H:64 + 2 * T * H].view(T, H))
+    act = olo.gate_up_silu(host(x), host(w)).astype(np.float16).astype(np.float64)
+    ref = act @ host(down).astype(np.float64).T
+    assert_close(out, ref, what="EngineMLP")

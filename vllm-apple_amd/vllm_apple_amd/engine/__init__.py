@@ -1,4 +1,4 @@
-"""Encode-only ops mirroring vllm_apple/engine/ops/{attention,kv_write,rmsnorm,elementwise,topk}.py.
+"""Encode-only ops mirroring vllm_apple/engine/ops/{attention,kv_write,rmsnorm,elementwise,topk,mlp}.py.
 
 "Encode" here means: enqueue the HIP kernels on a stream and return without
 waiting.  Every encode_* method keeps the reference's argument names and order;
@@ -10,12 +10,14 @@ the reference's (MTLBuffer, offset) pairs.
 from .attention import FusedAttentionParams, PagedAttentionOp, PagedAttentionParams
 from .elementwise import EngineElementwiseOps, EngineRoPE
 from .kv_write import KVWriteOp, KVWriteParams
+from .mlp import EngineMLP, MLPConfig
 from .rmsnorm import EngineRMSNorm, RMSNormConfig
 from .step import EngineStepContext
 from .topk import EngineTopK, reconstruct_logits
 
 __all__ = [
     "EngineElementwiseOps",
+    "EngineMLP",
     "EngineRMSNorm",
     "EngineRoPE",
     "EngineStepContext",
@@ -23,6 +25,7 @@ __all__ = [
     "FusedAttentionParams",
     "KVWriteOp",
     "KVWriteParams",
+    "MLPConfig",
     "PagedAttentionOp",
     "PagedAttentionParams",
     "RMSNormConfig",

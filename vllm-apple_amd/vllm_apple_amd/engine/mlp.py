@@ -1,0 +1,121 @@
+"""EngineMLP: mirror of vllm_apple/engine/ops/mlp.py's gated SiLU MLP on HIP.
+
+encode (mlp.py:170-245 with _encode_gated_mlp, :247-384) computes
+down_proj(silu(gate_proj(x)) * up_proj(x)).  The reference runs the gate and
+up GEMMs into two [T, I] intermediates and a silu_mul pass over them; here
+the first half is one MFMA kernel with the SwiGLU epilogue
+(kernels.gate_up_silu), so only the activated [T, I] intermediate exists, and
+the down projection is a plain library GEMM (torch.matmul on the step's
+stream).  Weights keep the reference's layouts: gate_proj / up_proj [I, H]
+or the fused gate_up_proj [2I, H] (gate rows first), down_proj [H, I].
+
+Only the gated SiLU form without biases is on this path; a standard MLP,
+GELU or biases raise NotImplementedError.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Dict, Optional
+
+import torch
+
+from .. import kernels
+from .step import resolve_stream, view
+
+
+@dataclass
+class MLPConfig:
+    hidden_size: int
+    intermediate_size: int
+    gated: bool = True
+    activation: str = "silu"
+    bias: bool = False
+
+
+class EngineMLP:
+    def __init__(self, context: Any, hidden_size: int, intermediate_size: int,
+                 gated: bool = True, activation: str = "silu", bias: bool = False):
+        if not gated or activation != "silu" or bias:
+            raise NotImplementedError("only the gated SiLU MLP without biases is supported")
+        self._context = context
+        self.config = MLPConfig(hidden_size=hidden_size, intermediate_size=intermediate_size,
+                                gated=gated, activation=activation, bias=bias)
+        self._gate_proj = None
+        self._up_proj = None
+        self._gate_up_proj = None
+        self._down_proj = None
+        self._fused_gate_up = False
+        self._scratch: Optional[torch.Tensor] = None
+
+    def set_weights(self, gate_proj: Optional[torch.Tensor] = None,
+                    up_proj: Optional[torch.Tensor] = None,
+                    down_proj: Optional[torch.Tensor] = None,
+                    gate_up_proj: Optional[torch.Tensor] = None,
+                    gate_bias: Optional[torch.Tensor] = None,
+                    up_bias: Optional[torch.Tensor] = None,
+                    down_bias: Optional[torch.Tensor] = None) -> None:
+        """mlp.py:125-168: a fused gate_up_proj takes precedence over separate
+        gate_proj / up_proj."""
+        if gate_bias is not None or up_bias is not None or down_bias is not None:
+            raise NotImplementedError("MLP biases are not supported")
+        if gate_up_proj is not None:
+            self._gate_up_proj, self._gate_proj, self._up_proj = gate_up_proj, None, None
+            self._fused_gate_up = True
+        else:
+            self._gate_proj, self._up_proj, self._gate_up_proj = gate_proj, up_proj, None
+            self._fused_gate_up = False
+        self._down_proj = down_proj
+
+    @staticmethod
+    def _buf(x: Any):
+        if isinstance(x, tuple):
+            return x
+        return x, 0
+
+    def _intermediate(self, num_tokens: int, like: torch.Tensor) -> torch.Tensor:
+        n = num_tokens * self.config.intermediate_size
+        if (self._scratch is None or self._scratch.numel() < n
+                or self._scratch.dtype != like.dtype or self._scratch.device != like.device):
+            self._scratch = torch.empty(n, dtype=like.dtype, device=like.device)
+        return self._scratch[:n].view(num_tokens, self.config.intermediate_size)
+
+    def encode(self, step_ctx: Any, hidden_states: Any, output_buffer: Any, num_tokens: int,
+               intermediate_buffer: Optional[Any] = None) -> None:
+        if self._down_proj is None:
+            raise RuntimeError("Down projection weights not set - call set_weights() first")
+        if not self._fused_gate_up and (self._gate_proj is None or self._up_proj is None):
+            raise RuntimeError("Gate and up projection weights not set for gated MLP. "
+                               "Call set_weights(gate_proj=..., up_proj=...) or "
+                               "set_weights(gate_up_proj=...)")
+        stream = resolve_stream(step_ctx)
+        H, I = self.config.hidden_size, self.config.intermediate_size
+        hb, ho = self._buf(hidden_states)
+        ob, oo = self._buf(output_buffer)
+        x = view(hb, ho, (num_tokens, H), dtype=hb.dtype)
+        out = view(ob, oo, (num_tokens, H), dtype=ob.dtype)
+        if intermediate_buffer is not None:
+            ib, io = self._buf(intermediate_buffer)
+            act = view(ib, io, (num_tokens, I), dtype=ib.dtype)
+        else:
+            act = self._intermediate(num_tokens, x)
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        with torch.cuda.stream(s):
+            if self._fused_gate_up:
+                kernels.gate_up_silu(x, self._gate_up_proj, out=act, stream=s)
+            else:
+                kernels.gate_up_silu(x, self._gate_proj, self._up_proj, out=act, stream=s)
+            torch.matmul(act, self._down_proj.t(), out=out)
+
+    def get_intermediate_size(self, num_tokens: int) -> int:
+        """Bytes of intermediate buffer encode needs: the one activated
+        [T, I] buffer (the reference needs three: gate, up and fused)."""
+        return num_tokens * self.config.intermediate_size * 2
+
+    def get_output_size(self, num_tokens: int) -> int:
+        return num_tokens * self.config.hidden_size * 2
+
+    def get_params_dict(self) -> Dict[str, Any]:
+        return {"hidden_size": self.config.hidden_size,
+                "intermediate_size": self.config.intermediate_size,
+                "gated": self.config.gated, "activation": self.config.activation,
+                "bias": self.config.bias}
