@@ -327,8 +327,8 @@ int vaa_silu_mul_2d(const uint16_t* gate, const uint16_t* up, uint16_t* output,
  * w_stride; output [num_tokens, intermediate_size] at row stride
  * output_stride (strides in elements).  hidden_size must be a multiple of
  * 64 and intermediate_size of 128 (VAA_ERR_UNSUPPORTED otherwise); x and
- * the weights 16-byte aligned with strides that are multiples of 8, the
- * output 8-byte aligned with a stride that is a multiple of 4.
+ * the weights and the output 16-byte aligned, with strides that are
+ * multiples of 8.
  */
 int vaa_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint16_t* w_gate,
                      const uint16_t* w_up, int64_t w_stride, uint16_t* output,

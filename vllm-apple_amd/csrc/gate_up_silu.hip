@@ -224,25 +224,45 @@ gate_up_silu_kernel(GluArgs a) {
   sink += pfa + pfb;
   if (sink == 0x7f7f7f7fu && a.num_tokens < 0) a.out[0] = 0;
 
-  // Epilogue.  The lane holds token xrow0 + 32c + l32 and, for row block f,
-  // columns 8 (r / 4) + 4 hb + r % 4 of that block: four runs of four
-  // consecutive columns, stored as 8-byte pieces.
+  // Epilogue, staged through LDS so that the output leaves in whole rows.
+  // The lane holds token xrow0 + 32c + l32 and, for row block f, columns
+  // 8 (r / 4) + 4 hb + r % 4 of that block: four runs of four consecutive
+  // columns.  silu(g) u is formed in registers and written as 8-byte pieces
+  // into a [256 tokens][128 columns] tile (token rows 0-127 in w0, 128-255
+  // in w1, 256 bytes each, 16-byte chunks XOR-swizzled by row & 15 so the 32
+  // token rows of one write hit distinct banks); then each row goes out as
+  // sixteen 16-byte stores.
+  __syncthreads();  // every wave is done with the operand tiles
+  char* stage = wt == 0 ? w0 : w1;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const int tok = t0 + xrow0 + 32 * c + l32;
-    if (tok >= a.num_tokens) continue;
-    char* orow = a.out + static_cast<int64_t>(tok) * a.os;
+    const int row = 32 * c + l32;  // within this wave's 128 token rows
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        const int col = i0 + 64 * wi + 32 * j + 8 * g4 + 4 * hb;
+        const int col = 64 * wi + 32 * j + 8 * g4 + 4 * hb;
         T v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = Elem<T>::from_f(silu_mul1(acc[j][c][4 * g4 + e], acc[2 + j][c][4 * g4 + e]));
-        *reinterpret_cast<u32x2*>(orow + 2 * col) = __builtin_bit_cast(u32x2, v);
+        const int chunk = (col >> 3) ^ (row & 15);
+        *reinterpret_cast<u32x2*>(stage + row * 256 + chunk * 16 + (col & 7) * 2) =
+            __builtin_bit_cast(u32x2, v);
       }
+  }
+  __syncthreads();
+  const int tid = threadIdx.x;
+  const int ch = tid & 15;
+#pragma unroll 4
+  for (int r0 = 0; r0 < kGT; r0 += kGThreads / 16) {
+    const int row = r0 + (tid >> 4);
+    const int tok = t0 + row;
+    if (tok < a.num_tokens) {
+      const char* src = (row < 128 ? w0 : w1) + (row & 127) * 256 + ((ch ^ (row & 15)) << 4);
+      *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(tok) * a.os + 2 * (i0 + 8 * ch)) =
+          *reinterpret_cast<const u32x4*>(src);
+    }
   }
 }
 
@@ -275,15 +295,13 @@ extern "C" int vaa_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint1
   if (num_tokens == 0) return VAA_OK;
   if (!x || !w_gate || !w_up || !output) return fail(VAA_ERR_INVALID_ARG, "%s: null pointer", what);
   if (x_stride < hidden_size || w_stride < hidden_size || output_stride < intermediate_size ||
-      x_stride % 8 != 0 || w_stride % 8 != 0 || output_stride % 4 != 0)
+      x_stride % 8 != 0 || w_stride % 8 != 0 || output_stride % 8 != 0)
     return fail(VAA_ERR_INVALID_ARG,
                 "%s: strides x=%lld w=%lld out=%lld (x, w: multiples of 8 >= hidden_size; out: "
-                "a multiple of 4 >= intermediate_size)",
+                "a multiple of 8 >= intermediate_size)",
                 what, (long long)x_stride, (long long)w_stride, (long long)output_stride);
-  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) ||
-      (reinterpret_cast<uintptr_t>(output) & 7u) != 0)
-    return fail(VAA_ERR_INVALID_ARG, "%s: x and weights must be 16-byte, output 8-byte aligned",
-                what);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(output))
+    return fail(VAA_ERR_INVALID_ARG, "%s: x, weights and output must be 16-byte aligned", what);
   GluArgs a;
   a.x = reinterpret_cast<const char*>(x);
   a.wg = reinterpret_cast<const char*>(w_gate);
