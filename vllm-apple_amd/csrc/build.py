@@ -41,8 +41,13 @@ ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")
 # v_max_f32 per score).  Scores are finite or the -inf of a masked key, so
 # the kernel is built without NaN semantics (infinities are kept): 3.5 %
 # faster on C3.
+#
+# The gate/up GEMM issues its direct-to-LDS loads as inline asm that writes
+# M0; clang warns that M0 is reserved because compiler-generated code may
+# use it, which that kernel's code does not.
 FILE_FLAGS = {
     "paged_prefill.hip": ["-fno-honor-nans"],
+    "gate_up_silu.hip": ["-Wno-inline-asm"],
 }
 
 

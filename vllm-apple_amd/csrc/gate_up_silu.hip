@@ -8,7 +8,7 @@
 // elementwise.py:114-124); here the epilogue reads g and u from the
 // accumulators, so neither intermediate is written or read back.
 //
-// Tiling (one 4-wave workgroup per CU, 128 KB of LDS):
+// Tiling (one 4-wave workgroup per CU, all 160 KB of LDS):
 //   workgroup = 256 tokens x 128 output columns: a 256 x 256 product of the
 //               token rows of x against 256 weight rows (128 gate, then the
 //               128 up rows of the same columns);
@@ -27,12 +27,15 @@
 // Memory: both operands are rows contiguous in the hidden dimension.  They
 // move from HBM to LDS with direct loads (buffer_load_dwordx4 ... lds: lane i
 // of a wave writes LDS bytes [16i, 16i + 16) after the wave-uniform base in
-// M0), double-buffered in four distinct LDS arrays, so the next k-step
-// streams in during this step's MFMAs; its 16 loads per wave are spread one
-// after every second MFMA of the step's first half.  Each wave also touches
-// the weight rows of the step kPfDist ahead with one 4-byte load per row,
-// which pulls them from HBM into L2 before the direct loads ask for them.
-// The 16-byte chunks of each 128-byte LDS row are XOR-swizzled by row & 7,
+// M0).  The loads are inline asm, so the compiler does not track them (it
+// would otherwise wait for every one of them before any LDS read); the
+// kernel orders each LDS read behind its own counted vmcnt wait and barrier.
+// Weight tiles go through a ring of three 32 KB stages and activation tiles
+// through two, all of LDS: during step k the wave issues the activation
+// loads of step k + 1 and then the weight loads of step k + 2, one load
+// after every second MFMA of the step's first half, so the weight stream,
+// which comes from HBM, has two steps to land and the activations, which
+// come from L2 and the Infinity Cache, one.  The 16-byte chunks of each 128-byte LDS row are XOR-swizzled by row & 7,
 // so the eight consecutive rows that an operand read spans per 128 bytes hit
 // distinct banks.  Token rows past num_tokens read the last token's row
 // (always in bounds) and their outputs are not stored.
@@ -60,7 +63,27 @@ static_assert(kGLoads == 8, "eight 1 KB direct loads per wave and operand");
 // no swizzle, offsets checked against the byte range in word 2.
 constexpr int kBufDword3 = 0x00020000;
 
-typedef __attribute__((address_space(3))) void lds_void_t;
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource for [base, base + bytes), in scalar registers.
+__device__ __forceinline__ i32x4v buffer_rsrc(const char* base, int bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4v r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((b >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = kBufDword3;
+  return r;
+}
+// One direct load of 16 bytes per lane into LDS: lane i writes bytes
+// [m0 + 16i, m0 + 16i + 16).  M0 is written here and used by nothing else
+// in this kernel.
+__device__ __forceinline__ void dma16(const i32x4v& rs, int voff, int soff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
+               :
+               : "v"(voff), "s"(m0), "s"(rs), "s"(soff)
+               : "memory", "m0");
+}
 
 struct GluArgs {
   const char* x;
@@ -71,20 +94,22 @@ struct GluArgs {
   int num_tokens, ksteps, t_tiles, tiles;
 };
 
-// s_waitcnt vmcnt(1) lgkmcnt(0), at the top of a k-step: every vector memory
-// load of this wave but the newest has landed.  Each step issues its 16
-// direct loads and then one L2 prefetch, and loads complete in issue order,
-// so the step's tiles are in LDS (as far as this wave's loads go; the barrier
-// that follows covers the other waves').
-__device__ __forceinline__ void glu_wait_tiles() { __builtin_amdgcn_s_waitcnt(0x0071); }
+// s_waitcnt vmcnt(8) lgkmcnt(0), at the top of step k: every vector memory
+// load of this wave but the newest 8 has landed.  Loads complete in issue
+// order and the newest 8 are the weights of step k + 1 (issued last in step
+// k - 1), so the activations of step k (issued before them) and the weights
+// of step k (issued in step k - 2) are in LDS, as far as this wave's loads
+// go; the barrier that follows covers the other waves'.
+__device__ __forceinline__ void glu_wait_tiles() { __builtin_amdgcn_s_waitcnt(0x0078); }
 
 template <typename T>
 __global__ void __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gate_up_silu_kernel(GluArgs a) {
-  __shared__ __align__(16) char w0[kGTileB];
-  __shared__ __align__(16) char w1[kGTileB];
-  __shared__ __align__(16) char x0[kGTileB];
-  __shared__ __align__(16) char x1[kGTileB];
+  __shared__ __align__(16) char smem[5 * kGTileB];  // W stages 0-2, x stages 0-1
+  char* const w0 = smem;
+  char* const w1 = smem + kGTileB;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)));
 
   const int per_xcd = static_cast<int>(gridDim.x) / kGXcds;
   const int logical = (static_cast<int>(blockIdx.x) % kGXcds) * per_xcd +
@@ -103,10 +128,8 @@ gate_up_silu_kernel(GluArgs a) {
   // weight matrix; its load q is 8 rows further on.  Every access stays
   // inside its resource's range (rows of x are clamped to num_tokens - 1).
   const char* wbase = (wave < 2 ? a.wg : a.wu) + static_cast<int64_t>(i0) * a.ws;
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(wbase), 0, static_cast<int>(kGI * a.ws), kBufDword3);
-  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(a.x), 0, static_cast<int>(a.num_tokens * a.xs), kBufDword3);
+  const i32x4v wrs = buffer_rsrc(wbase, static_cast<int>(kGI * a.ws));
+  const i32x4v xrs = buffer_rsrc(a.x, static_cast<int>(a.num_tokens * a.xs));
   const int rw = 8 * (wave & 1) * kGLoads + (lane >> 3);  // weight row of load 0, mod 128
   const int lc = (lane & 7) ^ (rw & 7);                    // a wave's rows agree mod 8
   const int woff = rw * static_cast<int>(a.ws) + lc * 16;
@@ -137,17 +160,14 @@ gate_up_silu_kernel(GluArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[f][c][r] = 0.f;
 
-  // Direct load q (0-7 weights, 8-15 activations) of the k-step at byte
-  // offset kb into the tiles wd, xd.
-  auto load1 = [&](int q, int kb, char* wd, char* xd) {
-    if (q < kGLoads)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void_t*)(wd + dst0 + 1024 * q), 16,
-                                               woff, kb + q * wstep, 0, 0);
+  // Direct load L of a step: 0-7 the activation tile of k-step kx into the
+  // LDS address xst, 8-15 the weight tile of k-step kw into wst.
+  auto load1 = [&](int L, int kbx, int kbw, uint32_t xst, uint32_t wst) {
+    if (L < kGLoads)
+      dma16(xrs, xoff[L], kbx, xst + dst0 + 1024 * L);
     else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xrs, (lds_void_t*)(xd + dst0 + 1024 * (q - kGLoads)), 16, xoff[q - kGLoads], kb, 0, 0);
+      dma16(wrs, woff, kbw + (L - kGLoads) * wstep, wst + dst0 + 1024 * (L - kGLoads));
   };
-  // Operand fragments of sub-step s (16 hidden elements per MFMA).
   auto frags = [&](const char* wt_, const char* xt_, int s, u32x4 (&A)[4], u32x4 (&B)[4]) {
 #pragma unroll
     for (int f = 0; f < 4; ++f)
@@ -156,73 +176,57 @@ gate_up_silu_kernel(GluArgs a) {
     for (int c = 0; c < 4; ++c)
       B[c] = *reinterpret_cast<const u32x4*>(xt_ + (xrow0 + 32 * c) * kGRowB + rd[s]);
   };
-  // The 16 MFMAs of one sub-step; with ld, direct loads q0 .. q0 + 7, one
-  // after every second MFMA (scheduling fences keep that order).
-  auto mfmas = [&](const u32x4 (&A)[4], const u32x4 (&B)[4], bool ld, int q0, int kb,
-                   char* wd, char* xd) {
+  auto mfmas = [&](const u32x4 (&A)[4], const u32x4 (&B)[4], bool ld, int L0, int kbx, int kbw,
+                   uint32_t xst, uint32_t wst) {
 #pragma unroll
     for (int idx = 0; idx < 16; ++idx) {
       const int f = idx >> 2, c = idx & 3;
       acc[f][c] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, A[f]),
                                         __builtin_bit_cast(typename Elem<T>::x8, B[c]),
                                         acc[f][c]);
-      if (ld && (idx & 1)) load1(q0 + (idx >> 1), kb, wd, xd);
+      if (ld && (idx & 1)) load1(L0 + (idx >> 1), kbx, kbw, xst, wst);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // L2 prefetch of the weight rows kPfDist steps ahead: one 4-byte load per
-  // row (one 128-byte line per row and step) of the wave's 64.  The values
-  // are summed into `sink` two steps later, when the wait at the top of the
-  // step has already covered them, and `sink` is kept alive by a store that
-  // never happens, so the loads are not dropped.
-  constexpr int kPfDist = 3;
-  const int pfw = (64 * (wave & 1) + lane) * static_cast<int>(a.ws);
-  uint32_t sink = 0, pfa = 0, pfb = 0;
-  auto prefetch = [&](int ks, uint32_t& slot) {
-    sink += slot;
-    slot = __builtin_amdgcn_raw_buffer_load_b32(wrs, pfw, min(ks + kPfDist, a.ksteps - 1) * kGRowB,
-                                                0);
-  };
-  // Step ks on the tiles (cw, cx): wait for them (this wave's loads, then
-  // everyone's through the barrier, which also retires every read of the
-  // other tiles in step ks - 1), then the four sub-steps with the next
-  // sub-step's operands read while this one's MFMAs run, and step ks + 1's
-  // loads (clamped to the last step: past the end they refill tiles that are
-  // not read again) into (nw, nx) among the first 32 MFMAs.
-  auto step = [&](int ks, const char* cw, const char* cx, char* nw, char* nx, uint32_t& slot) {
+  const int n = a.ksteps;
+  // Step ks: weights in W stage ks % 3, activations in x stage ks % 2; it
+  // loads the activations of step ks + 1 and then the weights of ks + 2.
+  auto step = [&](int ks) {
     glu_wait_tiles();
     __syncthreads();
-    const int kb = min(ks + 1, a.ksteps - 1) * kGRowB;
+    const char* cw = smem + (ks % 3) * kGTileB;
+    const char* cx = smem + (3 + (ks & 1)) * kGTileB;
+    const uint32_t xst = lds0 + (3 + ((ks + 1) & 1)) * kGTileB;
+    const uint32_t wst = lds0 + ((ks + 2) % 3) * kGTileB;
+    const int kbx = min(ks + 1, n - 1) * kGRowB;
+    const int kbw = min(ks + 2, n - 1) * kGRowB;
     u32x4 A0[4], B0[4], A1[4], B1[4];
     frags(cw, cx, 0, A0, B0);
     frags(cw, cx, 1, A1, B1);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(A0, B0, true, 0, kb, nw, nx);
+    mfmas(A0, B0, true, 0, kbx, kbw, xst, wst);
     frags(cw, cx, 2, A0, B0);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(A1, B1, true, 8, kb, nw, nx);
-    prefetch(ks, slot);
+    mfmas(A1, B1, true, 8, kbx, kbw, xst, wst);
     frags(cw, cx, 3, A1, B1);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(A0, B0, false, 0, kb, nw, nx);
-    mfmas(A1, B1, false, 0, kb, nw, nx);
+    mfmas(A0, B0, false, 0, 0, 0, 0, 0);
+    mfmas(A1, B1, false, 0, 0, 0, 0, 0);
   };
-
-  // Step 0's loads, then one prefetch so that the wait count holds from the
-  // first step.
+  // Prologue: weights of steps 0 and 1, activations of step 0, issued so
+  // that at the top of every step the newest 8 loads are the only ones that
+  // may still be in flight (the weights of the next step).
 #pragma unroll
-  for (int q = 0; q < 2 * kGLoads; ++q) load1(q, 0, w0, x0);
-  prefetch(-1, pfb);
-  int ks = 0;
-  for (; ks + 2 <= a.ksteps; ks += 2) {
-    step(ks, w0, x0, w1, x1, pfa);
-    step(ks + 1, w1, x1, w0, x0, pfb);
-  }
-  if (ks < a.ksteps) step(ks, w0, x0, w1, x1, pfa);
+  for (int q = 0; q < kGLoads; ++q) dma16(wrs, woff, q * wstep, lds0 + dst0 + 1024 * q);
+#pragma unroll
+  for (int q = 0; q < kGLoads; ++q)
+    dma16(xrs, xoff[q], 0, lds0 + 3 * kGTileB + dst0 + 1024 * q);
+#pragma unroll
+  for (int q = 0; q < kGLoads; ++q)
+    dma16(wrs, woff, min(1, n - 1) * kGRowB + q * wstep, lds0 + kGTileB + dst0 + 1024 * q);
+  for (int ks = 0; ks < n; ++ks) step(ks);
   // Every load has landed before the workgroup ends and its LDS is released.
   __builtin_amdgcn_s_waitcnt(0x0070);
-  sink += pfa + pfb;
-  if (sink == 0x7f7f7f7fu && a.num_tokens < 0) a.out[0] = 0;
 
   // Epilogue, staged through LDS so that the output leaves in whole rows.
   // The lane holds token xrow0 + 32c + l32 and, for row block f, columns
