@@ -2,8 +2,8 @@
 against the oracle (fp64 products, silu_mul of the unrounded values) within
 the north-star tolerance, and against the reference's unfused order (two
 GEMMs rounded to 16 bits, then silu_mul) within the rounding that the fusion
-removes.  Covers 1, 2, 3, 5 and 7 k-steps (odd counts
-end on the first of the two LDS buffers), token counts that leave a
+removes.  Covers 1, 2, 3, 5 and 7 k-steps (every end
+position of the three-stage weight ring and the two-stage activation ring), token counts that leave a
 partial token tile, fused and separate weights, strided rows and the C5 shape.
 """
 import numpy as np
