@@ -23,10 +23,11 @@
  * The innermost (head_size) dimension must be contiguous.
  *
  * Device-side guards: every kernel skips (never dereferences) a block id
- * outside [0, num_blocks) and a slot outside [0, num_blocks*block_size), so a
- * bad index cannot fault the GPU.  Range validation that raises errors is
- * done on the host by the Python layer, as the reference does
- * (vllm_apple/engine/kv_cache.py:300-420).
+ * outside [0, num_blocks), a slot outside [0, num_blocks*block_size) and a
+ * token offset whose write would leave its block, so a bad index cannot
+ * fault the GPU or write outside the block it names.  Range validation that
+ * raises errors is done on the host by the Python layer, as the reference
+ * does (vllm_apple/engine/kv_cache.py:300-420).
  */
 #ifndef VLLM_APPLE_AMD_H_
 #define VLLM_APPLE_AMD_H_
@@ -85,7 +86,7 @@ typedef struct vaa_attn_params {
   int32_t block_size;         /* tokens per cache block, multiple of 16       */
   int32_t num_kv_heads;
   int32_t num_query_heads;
-  int32_t queries_per_kv;     /* num_query_heads / num_kv_heads, <= 16        */
+  int32_t queries_per_kv;     /* num_query_heads / num_kv_heads               */
   int32_t partition_size;     /* split-K tokens per partition; 0 = automatic,
                                  VAA_PARTITION_BALANCED(_SHARED) = split by
                                  lengths                                      */
@@ -115,8 +116,11 @@ int vaa_abi_version(void);
  * Source K/V are contiguous [num_tokens, num_kv_heads, head_size]; for each
  * token t and head h the head_size elements go to
  * block_ids[t]*stride_block + h*stride_head + token_offsets[t]*stride_token.
- * Tokens whose block id is outside [0, num_blocks) or whose offset is
- * negative are skipped.
+ * The reference trusts both indices.  Here a token is skipped when its block
+ * id is outside [0, num_blocks) or its offset o is negative or so large that
+ * the token's write leaves the block:
+ *   o*stride_token + (num_kv_heads-1)*stride_head + head_size > stride_block
+ * (for both cache layouts that is o >= block_size).
  */
 int vaa_write_kv_batch(uint16_t* key_dst, uint16_t* value_dst,
                        const uint16_t* key_src, const uint16_t* value_src,
@@ -127,7 +131,9 @@ int vaa_write_kv_batch(uint16_t* key_dst, uint16_t* value_dst,
 
 /*
  * Replaces metal_write_kv_single (vllm_apple/metal/native/kv_write.c:84-107):
- * one token, block id and offset passed by value.
+ * one token, block id and offset passed by value.  Since both are host
+ * values, a block id or offset that vaa_write_kv_batch would skip is
+ * rejected with VAA_ERR_INVALID_ARG and nothing is enqueued.
  */
 int vaa_write_kv_single(uint16_t* key_dst, uint16_t* value_dst,
                         const uint16_t* key_src, const uint16_t* value_src,
@@ -201,6 +207,30 @@ int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
                                const uint16_t* new_keys,
                                const uint16_t* new_values, void* workspace,
                                size_t workspace_bytes, void* stream);
+
+/*
+ * Merge of attention states: the split-K second pass on its own, for partial
+ * results the caller computed (partitions of one context decoded apart, a
+ * context split across GPUs, a shared prefix and a per-request suffix).  No
+ * counterpart in the reference, whose kernels never split a context; the
+ * arithmetic is that of vaa_paged_attention_decode's merge pass.
+ *   partial_out  fp32 [num_seqs, num_heads, max_parts, head_size], each
+ *                partition's normalised output o_p (contiguous);
+ *   partial_lse  fp32 [num_seqs, num_heads, max_parts], lse_p = log of the
+ *                partition's softmax denominator, sum_j e^(scale q.k_j), in
+ *                natural log; -inf for a partition without keys;
+ *   num_parts    int32 [num_seqs]: partitions of each sequence (the first
+ *                num_parts[s] of max_parts), or null for all max_parts.
+ * out[s, h, :] = sum_p e^(lse_p - LSE) o_p with LSE = log sum_p e^(lse_p),
+ * rounded to the 16-bit dtype at strides (o_stride_token, o_stride_head); a
+ * row with no keys is zero.  output_lse (fp32 [num_seqs, num_heads], may be
+ * null) receives LSE (-inf for no keys), so merges can be chained.
+ */
+int vaa_merge_attn_states(const float* partial_out, const float* partial_lse,
+                          const int32_t* num_parts, int num_seqs, int num_heads,
+                          int max_parts, int head_size, uint16_t* output,
+                          int64_t o_stride_token, int64_t o_stride_head, float* output_lse,
+                          int dtype, void* stream);
 
 /*
  * Chunked-prefill paged attention (MFMA).  Replaces paged_attention_v2_prefill

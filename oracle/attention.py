@@ -13,6 +13,18 @@ prefill           numpy fp64.  Follows paged_attention_v2.metal:375-478: token t
                   [0, positions[t]]; rows with an invalid sequence, negative
                   position, context past the block table (:401) or an invalid
                   block inside the context (:428) are not written.
+decode_partials   numpy fp64: the decode restricted to key partitions
+                  [P*p, P*(p+1)) of each sequence, as (normalised partial
+                  output, natural-log softmax denominator); the input of a
+                  split-K merge.  No reference counterpart (the reference
+                  never splits a context).
+merge_states      numpy fp64 log-sum-exp merge of such partials:
+                  out = sum_p e^(lse_p - LSE) o_p, LSE = log sum_p e^(lse_p).
+                  Pinned by: merging decode_partials gives `decode` for any
+                  partition size (the split is exact in real arithmetic); one
+                  partition returns its o_p unchanged; a hand-computed
+                  two-partition case (weights 1/4, 3/4); empty partitions
+                  (lse -inf) are ignored.
 decode_loop_fp32  pure-Python fp32 loop with the exact structure of the Metal
                   kernel's online softmax (paged_attention_fused.metal:141-200);
                   small cases only.  Used to pin `decode`.
@@ -94,6 +106,62 @@ def decode(query: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
         V = np.where(valid[:, None, None], V, 0.0)
         out[s] = _attend(query[s:s + 1], K, V, valid, scale, G)[0]
     return out
+
+
+def decode_partials(query: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                    block_table: np.ndarray, seq_lens: np.ndarray, scale: float,
+                    part_tokens: int, layout: str = "kernel") -> tuple:
+    """(partial_out [S, H, P, D], lse [S, H, P], num_parts [S]) in fp64 for
+    partitions of part_tokens keys; P = the most partitions of any sequence.
+    Partitions past a sequence's length hold lse = -inf and zeros."""
+    nb, kv, bs, d = _layout_dims(k_cache, layout)
+    S, H, _ = query.shape
+    G = H // kv
+    cap = block_table.shape[1] * bs
+    lens = [max(0, min(int(x), cap)) for x in seq_lens]
+    nparts = [(L + part_tokens - 1) // part_tokens for L in lens]
+    P = max(max(nparts, default=0), 1)
+    out = np.zeros((S, H, P, d))
+    lse = np.full((S, H, P), -np.inf)
+    kvh = np.arange(H) // G
+    for s in range(S):
+        L = lens[s]
+        if L <= 0:
+            continue
+        K, valid = gather(k_cache, block_table[s], L, layout)
+        V, _ = gather(v_cache, block_table[s], L, layout)
+        V = np.where(valid[:, None, None], V, 0.0)
+        sc = np.einsum("hd,lhd->hl", query[s].astype(np.float64), K[:, kvh, :]) * scale
+        sc = np.where(valid[None, :], sc, -np.inf)
+        for p in range(nparts[s]):
+            lo, hi = p * part_tokens, min(L, (p + 1) * part_tokens)
+            x = sc[:, lo:hi]
+            m = x.max(axis=1, keepdims=True)
+            ok = np.isfinite(m[:, 0])
+            e = np.exp(x - np.where(np.isfinite(m), m, 0.0))
+            l = e.sum(axis=1)
+            o = np.einsum("hl,lhd->hd", e, V[lo:hi][:, kvh, :])
+            out[s, :, p] = np.where(ok[:, None], o / np.where(l > 0, l, 1.0)[:, None], 0.0)
+            lse[s, :, p] = np.where(ok, m[:, 0] + np.log(np.where(l > 0, l, 1.0)), -np.inf)
+    return out, lse, np.asarray(nparts, dtype=np.int32)
+
+
+def merge_states(partial_out: np.ndarray, lse: np.ndarray,
+                 num_parts: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """fp64 (out [S, H, D], LSE [S, H]) of partial states [S, H, P, D] / [S, H, P]."""
+    S, H, P, _ = partial_out.shape
+    use = np.ones((S, H, P), dtype=bool)
+    if num_parts is not None:
+        use &= (np.arange(P)[None, None, :] < np.asarray(num_parts)[:, None, None])
+    x = np.where(use & np.isfinite(lse), lse.astype(np.float64), -np.inf)
+    M = x.max(axis=2, keepdims=True)
+    has = np.isfinite(M)
+    w = np.where(has, np.exp(x - np.where(has, M, 0.0)), 0.0)
+    den = w.sum(axis=2)
+    out = np.einsum("shp,shpd->shd", w, partial_out.astype(np.float64))
+    out = np.where(den[..., None] > 0, out / np.where(den > 0, den, 1.0)[..., None], 0.0)
+    LSE = np.where(den > 0, M[..., 0] + np.log(np.where(den > 0, den, 1.0)), -np.inf)
+    return out, LSE
 
 
 def prefill(query: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,

@@ -6,6 +6,9 @@ Functions and the reference lines they follow
   kv_write_decode    paged_attention_fused.metal:55-101, kv_write.py:86-99 guards
   token_index        vllm_apple/engine/runner.py:526-546, apple_model_runner.py:1188-1200
   slot_mapping       vllm_apple/v1/worker/apple_model_runner.py:1202-1249
+  write_kv_batch     kv_write.c:33-78 with the library's index guard (block id
+                     outside the pool, offset whose write leaves the block:
+                     skipped)
   ref_write_kv_batch the reference's metal_write_kv_batch itself (kv_write.c:33-78)
 Pinned by tests/test_oracle_kv.py.
 """
@@ -45,8 +48,10 @@ def lib() -> ctypes.CDLL:
         l.oracle_kv_write_decode.argtypes = [_P, _P, _P, _I, _P, _I, _P, _P, _I, _I, _I, _I64, _I64, _I64, _I64, _I64, _I64]
         l.oracle_token_index.argtypes = [_P, _P, _I, _I, _P, _P]
         l.oracle_slot_mapping.argtypes = [_P, _I, _I, _P, _P, _I, _I, _P]
+        l.oracle_write_kv_batch.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I64, _I64,
+                                            _I64, _I64]
         for f in (l.oracle_kv_write_slots, l.oracle_kv_write_decode, l.oracle_token_index,
-                  l.oracle_slot_mapping):
+                  l.oracle_slot_mapping, l.oracle_write_kv_batch):
             f.restype = None
         _oracle = l
     return _oracle
@@ -140,6 +145,20 @@ def slot_mapping(block_table: np.ndarray, block_size: int, token_to_seq: np.ndar
     lib().oracle_slot_mapping(_p(bt), bt.shape[1], block_size, _p(tok), _p(pos), bt.shape[0],
                               tok.shape[0], _p(out))
     return out
+
+
+def write_kv_batch(k_cache: np.ndarray, v_cache: np.ndarray, key: np.ndarray,
+                   value: np.ndarray, block_ids: np.ndarray, token_offsets: np.ndarray,
+                   stride_block: int, stride_head: int, stride_token: int,
+                   num_blocks: int) -> None:
+    """Guarded metal_write_kv_batch on host arrays (see oracle_write_kv_batch)."""
+    key = np.ascontiguousarray(key)
+    value = np.ascontiguousarray(value)
+    bids = np.ascontiguousarray(block_ids, dtype=np.int64)
+    offs = np.ascontiguousarray(token_offsets, dtype=np.int64)
+    T, KV, D = key.shape
+    lib().oracle_write_kv_batch(_p(k_cache), _p(v_cache), _p(key), _p(value), _p(bids), _p(offs),
+                                T, KV, D, stride_block, stride_head, stride_token, num_blocks)
 
 
 def ref_write_kv_batch(k_cache: np.ndarray, v_cache: np.ndarray, key: np.ndarray,

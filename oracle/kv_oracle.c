@@ -36,6 +36,30 @@ void oracle_kv_write_slots(uint16_t* kc, uint16_t* vc, const int64_t* slots,
   }
 }
 
+/* metal_write_kv_batch (vllm_apple/metal/native/kv_write.c:33-78): token t,
+ * head h goes to block_ids[t]*sb + h*sh + offsets[t]*st.  The reference
+ * trusts both indices; the library's contract (and this restatement) skips a
+ * token whose block id is outside [0, num_blocks) or whose offset o is
+ * negative or makes the write end past the block: o*st + (KV-1)*sh + D > sb.
+ * In-range tokens are the reference's memcpy loop exactly. */
+void oracle_write_kv_batch(uint16_t* kc, uint16_t* vc, const uint16_t* k,
+                           const uint16_t* v, const int64_t* block_ids,
+                           const int64_t* offsets, int T, int KV, int D,
+                           int64_t sb, int64_t sh, int64_t st,
+                           int64_t num_blocks) {
+  for (int t = 0; t < T; ++t) {
+    const int64_t b = block_ids[t], o = offsets[t];
+    if (b < 0 || b >= num_blocks || o < 0) continue;
+    if (o * st + (int64_t)(KV - 1) * sh + D > sb) continue;
+    for (int h = 0; h < KV; ++h) {
+      const int64_t dst = b * sb + h * sh + o * st;
+      const int64_t src = ((int64_t)t * KV + h) * D;
+      memcpy(kc + dst, k + src, (size_t)D * 2);
+      memcpy(vc + dst, v + src, (size_t)D * 2);
+    }
+  }
+}
+
 /* kv_write_decode (paged_attention_fused.metal:55-101 with the guards of
  * vllm_apple/engine/ops/kv_write.py:86-99): position seq_len-1. */
 void oracle_kv_write_decode(uint16_t* kc, uint16_t* vc, const int32_t* bt,

@@ -242,3 +242,36 @@ def test_balanced_shared_workspace(lib):
     assert two > one > 0
     p.partition_size = -3
     assert lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part)) == 0
+
+
+def test_wide_groups_and_merge_arguments(lib):
+    """GQA groups above 16 heads have a workspace size (head chunks), the
+    state merge checks its arguments, and the single-token KV write rejects an
+    offset or block outside the pool before any launch."""
+    from vllm_apple_amd import _lib
+
+    p = _lib.VaaAttnParams()
+    p.head_size, p.block_size, p.num_kv_heads, p.num_query_heads = 128, 16, 1, 48
+    p.queries_per_kv, p.num_seqs, p.max_blocks_per_seq, p.num_blocks = 48, 4, 64, 256
+    p.max_seq_len = 1024
+    part = ctypes.c_int32(0)
+    p.partition_size = 128
+    n = lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part))
+    assert n == 4 * 48 * 8 * 130 * 4 and part.value == 128
+    p.partition_size = -1
+    n = lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part))
+    assert n > 0
+    st = lib.vaa_merge_attn_states(None, None, None, 2, 0, 4, 128, None, 0, 0, None, 0, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG
+    st = lib.vaa_merge_attn_states(None, None, None, 2, 4, 4, 128, None, 0, 0, None, 9, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED
+    assert lib.vaa_merge_attn_states(None, None, None, 0, 4, 4, 128, None, 0, 0, None, 0,
+                                     None) == 0
+    buf = ctypes.create_string_buffer(64)
+    a = ctypes.addressof(buf)
+    # kernel layout, KV 2, bs 16, D 64: offsets 0..15 are inside a block.
+    sb, sh, st_ = 2 * 16 * 64, 16 * 64, 64
+    for b, o in ((3, 16), (3, -1), (-1, 0), (8, 0)):
+        st = lib.vaa_write_kv_single(a, a, a, a, b, o, 2, 64, sb, sh, st_, 8, None)
+        assert st == _lib.VAA_ERR_INVALID_ARG, (b, o)
+        assert "vaa_write_kv_single" in _lib.last_error()

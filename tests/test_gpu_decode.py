@@ -212,3 +212,102 @@ def test_decode_balanced_workspace_reuse(gpu):
                                    partition_size=-2 if S == 7 else -1, workspace=ws)
         ref = oat.decode(host(q), host(kc), host(vc), host(bt), host(L), 1 / np.sqrt(128))
         assert_close(host(out), ref, what=f"balanced reuse S={S}")
+
+
+def test_decode_graph_replay_after_workspace_growth(gpu):
+    """A decode captured in a HIP graph keeps working after a later eager call
+    grows the shared split-K workspace: the outgrown buffer stays allocated,
+    so the replay neither reads freed memory nor writes into a tensor that
+    was allocated after the growth."""
+    from vllm_apple_amd import kernels
+
+    torch.cuda.synchronize()
+    small = [900, 1500, 300]
+    kc, vc, bt, L, q, nk, nv = _case(3, 32, 8, 128, small, seed=41)
+    kd, vd, btd, Ld, qd = kc.cuda(), vc.cuda(), bt.cuda(), L.cuda(), q.cuda()
+    out = torch.empty_like(qd)
+    kw = dict(scale=1 / np.sqrt(128), max_seq_len=max(small), partition_size=128)
+
+    def step():
+        kernels.paged_decode(qd, kd, vd, btd, Ld, output=out, **kw)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # warm-up: sizes the workspace for this call
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    # A longer eager decode needs a bigger workspace: the shared one grows.
+    # Each 65536-token sequence needs 32 heads x 512 partitions x 130 floats.
+    before = kernels.decode_workspace(0, qd.device)
+    per_seq = 32 * 512 * 130 * 4
+    n_big = before.numel() // per_seq + 1
+    big = [65536 - 7 * i for i in range(n_big)]
+    kc2, vc2, bt2, L2, q2, *_ = _case(n_big, 32, 2, 128, big, seed=42)
+    kernels.paged_decode(q2.cuda(), kc2.cuda(), vc2.cuda(), bt2.cuda(), L2.cuda(),
+                         scale=1 / np.sqrt(128), max_seq_len=max(big), partition_size=128)
+    torch.cuda.synchronize()
+    assert kernels.decode_workspace(0, qd.device).data_ptr() != before.data_ptr(), "no growth"
+    del kc2, vc2, bt2, L2, q2, before
+    # Tensors allocated after the growth, which may reuse freed blocks.
+    sentinels = [torch.full((1 << 20,), 7.0, device="cuda") for _ in range(8)]
+    ref = oat.decode(host(q), host(kc), host(vc), host(bt), host(L), 1 / np.sqrt(128))
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_close(host(out), ref, what="graph replay after workspace growth")
+        for t in sentinels:
+            assert bool(torch.all(t == 7.0)), "a replay wrote into a later allocation"
+
+
+@pytest.mark.parametrize("H,KV,D", [(48, 1, 128), (32, 1, 64), (40, 2, 128), (17, 1, 96),
+                                    (64, 2, 32)])
+def test_decode_wide_groups(gpu, H, KV, D):
+    """GQA groups of more than 16 query heads (MQA with many heads): the group
+    runs in chunks of at most 16 heads, each its own workgroup, against the
+    oracle for the unsplit, fixed-partition and both balanced splits, with the
+    fused write bit-exact (only the first chunk writes the new token)."""
+    lens = [1, 16, 17, 700, 3000, 0, 4100]
+    print(f"[case] wide groups H={H} KV={KV} D={D}", flush=True)
+    kc, vc, bt, L, q, nk, nv = _case(len(lens), H, KV, D, lens, seed=50 + H)
+    for part in (0, 128, 1024, -1, -2):
+        out, ref, kd, vd, kr, vr = _run(kc, vc, bt, L, q, nk, nv, part=part)
+        assert_close(host(out), ref, what=f"decode H={H} KV={KV} D={D} part={part}")
+        assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16)), "fused K write"
+        assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16)), "fused V write"
+        assert torch.count_nonzero(out[5]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_merge_attn_states(gpu, dtype):
+    """vaa_merge_attn_states on partials of a split decode (computed exactly
+    on the host) against the unsplit decode and the oracle merge, with
+    ragged partition counts, empty sequences and chained LSE output."""
+    from vllm_apple_amd import kernels
+
+    lens = [0, 1, 300, 5000, 2047, 9000]
+    kc, vc, bt, L, q, *_ = _case(len(lens), 32, 8, 128, lens, seed=61)
+    scale = 1 / np.sqrt(128)
+    po, lse, n = oat.decode_partials(host(q), host(kc), host(vc), host(bt), host(L), scale, 512)
+    ref_out, ref_lse = oat.merge_states(po, lse, n)
+    full = oat.decode(host(q), host(kc), host(vc), host(bt), host(L), scale)
+    po_d = torch.from_numpy(po.astype(np.float32)).cuda()
+    lse_d = torch.from_numpy(lse.astype(np.float32)).cuda()
+    out_lse = torch.empty(lse.shape[:2], dtype=torch.float32, device="cuda")
+    out = kernels.merge_attn_states(po_d, lse_d, num_parts=torch.from_numpy(n).cuda(),
+                                    output_lse=out_lse, dtype=dtype)
+    torch.cuda.synchronize()
+    tol = dict(atol=2e-3) if dtype == torch.float16 else dict(atol=1.6e-2)
+    assert_close(out.float().cpu().numpy(), full, what="merge vs unsplit decode", **tol)
+    assert_close(out.float().cpu().numpy(), ref_out, what="merge vs oracle merge", **tol)
+    got_lse = out_lse.cpu().numpy()
+    assert np.all(np.isneginf(got_lse[0]))
+    assert np.allclose(got_lse[1:], ref_lse[1:], rtol=1e-5, atol=1e-5)
+    assert torch.count_nonzero(out[0]) == 0
+    # Without num_parts the -inf partitions past each length are skipped too.
+    out2 = kernels.merge_attn_states(po_d, lse_d, dtype=dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)

@@ -118,6 +118,47 @@ def test_write_kv_batch_matches_reference_c(gpu):
     assert np.array_equal(host(vd).view(np.uint16), vc_ref.view(np.uint16))
 
 
+@pytest.mark.parametrize("layout", ["kernel", "vllm"])
+def test_write_kv_batch_offset_guard(gpu, layout):
+    """Offsets at or past the block size aimed at a middle block (in-bounds
+    memory: without the guard they would land in the next block) are skipped,
+    as are negative offsets and blocks outside the pool; the valid tokens of
+    the same call are written bit-exactly; the single-token entry point
+    rejects such indices on the host."""
+    from vllm_apple_amd import kernels
+
+    nb, kv, bs, d = 16, 8, 16, 128
+    print(f"[case] write_kv_batch offset guard layout={layout}", flush=True)
+    kc, vc = _caches(nb, kv, bs, d, layout, 21)
+    sb, sh, st = okv.cache_strides(host(kc), layout)
+    g = torch.Generator().manual_seed(22)
+    T = 9
+    key = torch.randn(T, kv, d, generator=g).half()
+    val = torch.randn(T, kv, d, generator=g).half()
+    bids = torch.tensor([7, 7, 7, 7, -1, nb, 3, 7, nb - 1], dtype=torch.int64)
+    offs = torch.tensor([bs, bs + 1, 2 * bs - 1, -1, 0, 0, 4, bs - 1, bs], dtype=torch.int64)
+    kc_ref, vc_ref = host(kc).copy(), host(vc).copy()
+    okv.write_kv_batch(kc_ref, vc_ref, host(key), host(val), host(bids), host(offs), sb, sh, st, nb)
+    kd, vd = kc.cuda(), vc.cuda()
+    kernels.write_kv_batch(kd, vd, key.cuda(), val.cuda(), bids.cuda(), offs.cuda(), sb, sh, st, nb)
+    torch.cuda.synchronize()
+    got_k, got_v = host(kd).view(np.uint16), host(vd).view(np.uint16)
+    assert np.array_equal(got_k, kc_ref.view(np.uint16))
+    assert np.array_equal(got_v, vc_ref.view(np.uint16))
+    # Block 8 (the neighbour of block 7) is byte-identical to the input.
+    assert np.array_equal(got_k[8], host(kc).view(np.uint16)[8])
+    assert np.array_equal(got_v[8], host(vc).view(np.uint16)[8])
+    # Only blocks 3 and 7 changed (offsets 4 and bs - 1).
+    changed = np.nonzero((got_k != host(kc).view(np.uint16)).reshape(nb, -1).any(1))[0]
+    assert changed.tolist() == [3, 7]
+    for b, o in ((7, bs), (7, -1), (-1, 0), (nb, 0)):
+        with pytest.raises(ValueError, match="vaa_write_kv_single"):
+            kernels.write_kv_single(kd, vd, key[0].contiguous().cuda(), val[0].contiguous().cuda(),
+                                    b, o, sb, sh, st, nb)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(kd).view(np.uint16), got_k)
+
+
 def test_kv_write_empty_and_all_padding(gpu):
     from vllm_apple_amd import kernels
 

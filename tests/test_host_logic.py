@@ -62,6 +62,15 @@ def test_descriptor_rules():
     d = KVCacheDescriptor(10, 16, 8, 128, 2)
     assert d.block_size_bytes == 8 * 16 * 128 * 2 * 2
     assert d.total_cache_bytes == d.block_size_bytes * 10 * 2
+    # bf16 blocks are as large as fp16 ones, and the sizes equal what
+    # HipKVCache allocates (the reference's formula counted 4 bytes for
+    # anything not fp16).
+    b = KVCacheDescriptor(10, 16, 8, 128, 2, dtype=torch.bfloat16)
+    assert b.block_size_bytes == d.block_size_bytes
+    c = HipKVCache(b, device="cpu", zero=False)
+    k, v = c.get_buffers(0)
+    assert b.total_cache_bytes == c._storage.numel() * c._storage.element_size()
+    assert b.block_size_bytes == (k[0].numel() + v[0].numel()) * k.element_size()
 
 
 def test_strides_match_reference():
@@ -153,8 +162,12 @@ def test_impl_error_conventions():
         _impl(kv_cache_dtype="fp8")
     with pytest.raises(ValueError):
         _impl(head_size=80)
-    impl = _impl(sliding_window=4096)
-    assert impl.sliding_window == (4095, 0)
+    # A sliding window would be ignored by the kernels: refused, not silently
+    # attended over the whole context.
+    with pytest.raises(NotImplementedError, match="sliding_window"):
+        _impl(sliding_window=4096)
+    impl = _impl()
+    assert impl.sliding_window == (-1, -1)
     q = torch.zeros(2, 32, 128, dtype=torch.float16)
     out = torch.ones_like(q)
     with pytest.raises(AssertionError):

@@ -107,6 +107,50 @@ def test_decode_closed_forms():
     np.testing.assert_allclose(got2[0, 0], vc2[blk, 0, off].astype(np.float64), atol=1e-9)
 
 
+@pytest.mark.parametrize("part", [16, 100, 512, 4096])
+def test_merge_of_partials_is_decode(part):
+    """Splitting each context into partitions and merging their states gives
+    the unsplit decode: exact in real arithmetic for any partition size, so
+    a dropped weight, a wrong sign in the exponent or a missing normalisation
+    fails.  Wide groups (G = 20) and empty sequences included."""
+    lens = [0, 1, 15, 700, 3001]
+    kc, vc, bt, L, q = _paged(5, 40, 2, 64, lens, seed=31)
+    scale = 1 / 8
+    po, lse, n = oat.decode_partials(q, kc, vc, bt, L, scale, part)
+    got, LSE = oat.merge_states(po, lse, n)
+    ref = oat.decode(q, kc, vc, bt, L, scale)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    assert np.all(np.isneginf(LSE[0])) and not np.any(got[0])
+    # LSE of the whole context from the scores directly.
+    K, _ = oat.gather(kc, bt[4], lens[4], "kernel")
+    sc = np.einsum("hd,lhd->hl", q[4].astype(np.float64), K[:, np.arange(40) // 20]) * scale
+    direct = np.log(np.exp(sc - sc.max(1, keepdims=True)).sum(1)) + sc.max(1)
+    assert np.allclose(LSE[4], direct, rtol=1e-12)
+
+
+def test_merge_states_closed_forms():
+    rs = np.random.RandomState(3)
+    o = rs.randn(2, 3, 4, 8)
+    lse = rs.randn(2, 3, 4)
+    # One partition: unchanged.
+    got, LSE = oat.merge_states(o[:, :, :1], lse[:, :, :1])
+    assert np.array_equal(got, o[:, :, 0]) and np.allclose(LSE, lse[:, :, 0])
+    # lse 0 and ln 3: weights 1/4 and 3/4, LSE = ln 4.
+    two = np.stack([np.zeros((1, 1)), np.full((1, 1), math.log(3.0))], axis=-1)
+    got, LSE = oat.merge_states(o[:1, :1, :2], two)
+    assert np.allclose(got[0, 0], 0.25 * o[0, 0, 0] + 0.75 * o[0, 0, 1], rtol=1e-14)
+    assert np.isclose(LSE[0, 0], math.log(4.0))
+    # Empty partitions (-inf) and partitions past num_parts are ignored.
+    l2 = lse.copy()
+    l2[:, :, 2] = -np.inf
+    a, _ = oat.merge_states(o, l2, np.array([4, 4]))
+    b, _ = oat.merge_states(np.delete(o, 2, axis=2), np.delete(lse, 2, axis=2))
+    assert np.allclose(a, b, rtol=1e-14)
+    c, _ = oat.merge_states(o, lse, np.array([3, 3]))
+    d, _ = oat.merge_states(o[:, :, :3], lse[:, :, :3])
+    assert np.array_equal(c, d)
+
+
 def test_prefill_without_prefix_is_causal_sdpa():
     kc, vc, bt, _, _ = _paged(1, 8, 2, 64, [40], seed=7)
     rs = np.random.RandomState(8)

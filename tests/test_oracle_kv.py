@@ -57,6 +57,46 @@ def test_slots_match_reference_c():
     assert np.array_equal(c_k.view(np.uint16), e_k.view(np.uint16))
 
 
+@pytest.mark.parametrize("layout", ["kernel", "vllm"])
+def test_write_kv_batch_guard(layout):
+    """oracle_write_kv_batch: in-range tokens are the reference's kv_write.c
+    byte for byte (on either layout's strides); a token with an offset at or
+    past the block size, a negative offset or a block outside the pool
+    changes nothing, not even the neighbouring block its row would reach."""
+    nb, kv, bs, d, T = 12, 4, 16, 64, 40
+    kc, vc = _cache(nb, kv, bs, d, layout, 11)
+    sb, sh, st = okv.cache_strides(kc, layout)
+    rs = np.random.RandomState(12)
+    key = rs.randn(T, kv, d).astype(np.float16)
+    val = rs.randn(T, kv, d).astype(np.float16)
+    slots = rs.permutation(nb * bs)[:T].astype(np.int64)
+    bids, offs = slots // bs, slots % bs
+    a_k, a_v = kc.copy(), vc.copy()
+    okv.write_kv_batch(a_k, a_v, key, val, bids, offs, sb, sh, st, nb)
+    e_k, e_v = kc.copy(), vc.copy()
+    okv.kv_write_slots(e_k, e_v, key, val, slots, layout)
+    assert np.array_equal(a_k.view(np.uint16), e_k.view(np.uint16))
+    assert np.array_equal(a_v.view(np.uint16), e_v.view(np.uint16))
+    if okv.ref_lib() is not None:
+        r_k, r_v = kc.copy(), vc.copy()
+        okv.ref_write_kv_batch(r_k, r_v, key, val, bids, offs, sb, sh, st)
+        assert np.array_equal(a_k.view(np.uint16), r_k.view(np.uint16))
+    # Bad indices: a middle block with offset bs and bs + 3 (the reference
+    # would write into block 6), offset -1, block -1 and block nb.
+    bad_b = np.array([5, 5, 5, -1, nb], dtype=np.int64)
+    bad_o = np.array([bs, bs + 3, -1, 0, 0], dtype=np.int64)
+    b_k, b_v = kc.copy(), vc.copy()
+    okv.write_kv_batch(b_k, b_v, key[:5], val[:5], bad_b, bad_o, sb, sh, st, nb)
+    assert np.array_equal(b_k.view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(b_v.view(np.uint16), vc.view(np.uint16))
+    # The last valid offset still writes, and only its own block.
+    c_k, c_v = kc.copy(), vc.copy()
+    okv.write_kv_batch(c_k, c_v, key[:1], val[:1], np.array([5]), np.array([bs - 1]), sb, sh, st,
+                       nb)
+    changed = np.nonzero((c_k.view(np.uint16) != kc.view(np.uint16)).reshape(nb, -1).any(1))[0]
+    assert changed.tolist() == [5]
+
+
 def test_slots_vllm_layout_match_torch_scatter():
     nb, kv, bs, d, T = 20, 2, 16, 64, 100
     kc, vc = _cache(nb, kv, bs, d, "vllm", 3)

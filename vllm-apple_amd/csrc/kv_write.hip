@@ -60,29 +60,45 @@ struct DecodeResolver {
   }
 };
 
-// Explicit (block id, offset) arrays (kv_write.c:50-57).
+// Explicit (block id, offset) arrays (kv_write.c:50-57).  The reference
+// trusts both; here a token is skipped unless 0 <= block < num_blocks and
+// 0 <= offset < off_limit, the offsets whose whole [KV, D] write stays inside
+// the block's stride_block elements (offset_limit()), so a bad offset can
+// neither spill into the neighbouring block nor past the last one.
 struct BatchResolver {
   const int64_t* block_ids;
   const int64_t* offsets;
   int64_t num_blocks;
+  int64_t off_limit;
   __device__ bool operator()(int t, int64_t& block, int64_t& off) const {
     int64_t b = block_ids[t], o = offsets[t];
-    if (b < 0 || b >= num_blocks || o < 0) return false;
+    if (b < 0 || b >= num_blocks || o < 0 || o >= off_limit) return false;
     block = b;
     off = o;
     return true;
   }
 };
 
+// One token whose block and offset the host has already checked.
 struct SingleResolver {
-  int64_t block_id, offset, num_blocks;
+  int64_t block_id, offset;
   __device__ bool operator()(int, int64_t& block, int64_t& off) const {
-    if (block_id < 0 || block_id >= num_blocks || offset < 0) return false;
     block = block_id;
     off = offset;
     return true;
   }
 };
+
+// Number of token offsets o >= 0 for which the write of one token,
+// elements [o*st, o*st + (kv-1)*sh + d) of its block, ends within the
+// block's sb elements: o*st + (kv-1)*sh + d <= sb.  0 when even offset 0
+// does not fit; unbounded (INT64_MAX) for a zero token stride.
+int64_t offset_limit(int64_t sb, int64_t sh, int64_t st, int kv, int d) {
+  const int64_t room = sb - static_cast<int64_t>(kv - 1) * sh - d;
+  if (room < 0) return 0;
+  if (st <= 0) return INT64_MAX;
+  return room / st + 1;
+}
 
 // VEC = 8: 16-byte chunks (all pointers/strides 8-element aligned);
 // VEC = 1: 2-byte fallback for unaligned views.
@@ -176,11 +192,14 @@ extern "C" int vaa_write_kv_batch(uint16_t* key_dst, uint16_t* value_dst,
   if (st) return st;
   if (num_tokens < 0 || (num_tokens > 0 && (!block_ids || !token_offsets)))
     return fail(VAA_ERR_INVALID_ARG, "vaa_write_kv_batch: bad token arrays");
+  if (stride_block < 0 || stride_head < 0 || stride_token < 0)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_write_kv_batch: negative stride");
   CacheDst d{key_dst, value_dst, stride_block, stride_head, stride_token,
              stride_block, stride_head, stride_token};
   NewSrc s{key_src, value_src, static_cast<int64_t>(num_kv_heads) * head_size,
            head_size};
-  BatchResolver r{block_ids, token_offsets, num_blocks};
+  BatchResolver r{block_ids, token_offsets, num_blocks,
+                  offset_limit(stride_block, stride_head, stride_token, num_kv_heads, head_size)};
   return launch_copy(d, s, r, num_tokens, num_kv_heads, head_size,
                      static_cast<hipStream_t>(stream), "vaa_write_kv_batch");
 }
@@ -195,11 +214,23 @@ extern "C" int vaa_write_kv_single(uint16_t* key_dst, uint16_t* value_dst,
   int st = check_common(num_kv_heads, head_size, key_dst, value_dst, key_src,
                         value_src, "vaa_write_kv_single");
   if (st) return st;
+  if (stride_block < 0 || stride_head < 0 || stride_token < 0)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_write_kv_single: negative stride");
+  // Both indices are host values: reject them here instead of skipping.
+  if (block_id < 0 || block_id >= num_blocks)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_write_kv_single: block_id=%lld outside [0, %lld)",
+                (long long)block_id, (long long)num_blocks);
+  const int64_t lim =
+      offset_limit(stride_block, stride_head, stride_token, num_kv_heads, head_size);
+  if (token_offset < 0 || token_offset >= lim)
+    return fail(VAA_ERR_INVALID_ARG,
+                "vaa_write_kv_single: token_offset=%lld outside the block (valid: 0..%lld)",
+                (long long)token_offset, (long long)lim - 1);
   CacheDst d{key_dst, value_dst, stride_block, stride_head, stride_token,
              stride_block, stride_head, stride_token};
   NewSrc s{key_src, value_src, static_cast<int64_t>(num_kv_heads) * head_size,
            head_size};
-  SingleResolver r{block_id, token_offset, num_blocks};
+  SingleResolver r{block_id, token_offset};
   return launch_copy(d, s, r, 1, num_kv_heads, head_size,
                      static_cast<hipStream_t>(stream), "vaa_write_kv_single");
 }

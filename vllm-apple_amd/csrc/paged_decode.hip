@@ -7,8 +7,11 @@
 // zero row for seq_len <= 0).
 //
 // Work decomposition
-//   grid     = (partition, kv_head, seq); one workgroup serves every query
-//              head of the GQA group, so each K/V byte is read from HBM once.
+//   grid     = (partition, kv_head x head chunk, seq); one workgroup serves
+//              every query head of the GQA group (up to 16, the MFMA columns),
+//              so each K/V byte is read from HBM once.  Larger groups (MQA
+//              with many heads) are cut into ceil(G/16) chunks of at most 16
+//              heads, one workgroup each.
 //   block    = 8 waves; each wave streams a contiguous run of 16-token tiles
 //              with its own (max, sum, acc) and the waves are combined in LDS
 //              at the end.  Fixed partitions of at most 1024 tokens and the
@@ -43,6 +46,8 @@
 // so the steady-state loop issues no scalar memory loads.
 #include "common.h"
 
+#include <atomic>
+
 namespace vaa {
 namespace {
 
@@ -66,13 +71,15 @@ struct DecodeArgs {
   // Split-K partials, one row per (piece, query head): unnormalised acc [D]
   // and (max in the log2 domain, sum).  Fixed partitions use rows
   // (seq*H + qhead)*max_parts + part; the balanced split uses
-  // (kvh*(max_parts + num_seqs) + c + seq)*G + h, with max_parts = workgroups
-  // per kv head, and keeps its geometry in ws_hdr (per, starts[0..num_seqs]).
+  // (y*(max_parts + num_seqs) + c + seq)*Gc + h, with y = kv head x head
+  // chunk, max_parts = workgroups per y, and keeps its geometry in ws_hdr
+  // (per, starts[0..num_seqs]).
   float* ws_acc;
   float* ws_ml;
   int* ws_hdr;
   float scale_log2;
   int num_seqs, max_blocks, block_size, num_kv_heads, num_q_heads, G;
+  int Gc, chunks;  // query heads per chunk (<= 16) and chunks per kv head
   int part_tiles, max_parts;
   int lds_main;  // bytes of LDS before the balanced split's prefix sums
   int64_t num_blocks;
@@ -203,19 +210,21 @@ struct RangeOut {
   int64_t prow_step;  // workspace row stride between the group's query heads
 };
 
-// The NW waves of the workgroup attend query heads kvh*G .. kvh*G+G-1 of
+// The NW waves of the workgroup attend query heads qh0 .. qh0+nh-1 (nh <= 16,
+// all of kv head kvh's group or a chunk of it) of
 // sequence seq over the 16-token tiles [t0, t1) of its first L (clamped)
 // positions: each wave streams a contiguous run of tiles, then the waves
 // combine through LDS.  smem is reused on return only after the trailing
 // barrier, so a workgroup may call this repeatedly.
 template <int D, typename T, int NW = kWaves>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
-                                             int kvh, int L, bool fused, int t0, int t1,
-                                             const RangeOut& ro, bool trailing_barrier) {
+                                             int kvh, int qh0, int nh, int L, bool fused,
+                                             bool write_new, int t0, int t1, const RangeOut& ro,
+                                             bool trailing_barrier) {
   using C = Cfg<D>;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int c16 = lane & 15, g = lane >> 4;
-  const int G = a.G;
+  const int G = nh;
   const int n_tiles = (L + kTile - 1) / kTile;
   const int per = (t1 - t0 + NW - 1) / NW;
   const int jb = t0 + wave * per;
@@ -248,7 +257,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   u32x4 qb[C::NS];
   {
     const bool hv = c16 < G;
-    const f16* qp = a.q + seq * a.q_st + (kvh * G + (hv ? c16 : 0)) * a.q_sh + g * (D / 4);
+    const f16* qp = a.q + seq * a.q_st + (qh0 + (hv ? c16 : 0)) * a.q_sh + g * (D / 4);
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) qb[s] = hv ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
   }
@@ -298,7 +307,9 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   }
 
   // Peeled last tile: partial and/or carrying the new token, which is read
-  // from new_k/new_v and written to the cache here (the fused KV write).
+  // from new_k/new_v and, when write_new, written to the cache here (the
+  // fused KV write; of the head chunks of one kv head only the first
+  // writes, the others read the same token from new_k/new_v).
   if (special >= jb && special < je) {
     const int j = special;
     const int tok0 = j * kTile;
@@ -318,7 +329,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
                            : kb + m.koff;
 #pragma unroll
       for (int s = 0; s < C::NS; ++s) t.k[s] = ld16(kp + 8 * s);
-      if (mine) {
+      if (mine && write_new) {
 #pragma unroll
         for (int s = 0; s < C::NS; ++s) st16(kb + m.koff + 8 * s, t.k[s]);
       }
@@ -329,7 +340,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
       const int ch = (i * kWave + lane) % C::CH;
       const f16* vp = mine ? a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8 : vb + m.voff[i];
       t.v[i] = ld16(vp);
-      if (mine) st16(vb + m.voff[i], t.v[i]);
+      if (mine && write_new) st16(vb + m.voff[i], t.v[i]);
     }
     tile_math<D, T>(m, t, qb, vt, valid, g, a.scale_log2, m_run, l_part, acc);
   }
@@ -376,7 +387,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
       }
     }
     if (ro.whole) {
-      const int qh = kvh * G + h;
+      const int qh = qh0 + h;
       reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
           Elem<T>::from_f(den > 0.f ? num / den : 0.f);
     } else {
@@ -413,12 +424,13 @@ template <int D, typename T, int NW>
 __global__ void __launch_bounds__(NW* kWave)
 paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-  const int G = a.G;
+  const int part = blockIdx.x, seq = blockIdx.z;
+  const int kvh = blockIdx.y / a.chunks, hc = blockIdx.y % a.chunks;
+  const int qh0 = kvh * a.G + hc * a.Gc, nh = min(a.Gc, a.G - hc * a.Gc);
   const int Lorig = a.seq_lens[seq];
   const int L = clamped_len(a, seq);
   if (L <= 0) {
-    if (part == 0) zero_rows(a, seq, kvh * G, G, D);
+    if (part == 0) zero_rows(a, seq, qh0, nh, D);
     return;
   }
   const int part_tok = a.part_tiles * kTile;
@@ -429,10 +441,10 @@ paged_decode_kernel(DecodeArgs a) {
   const int t1 = (part == a.max_parts - 1) ? n_tiles : min(t0 + a.part_tiles, n_tiles);
   RangeOut ro;
   ro.whole = (n_parts == 1);
-  ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + kvh * G) * a.max_parts + part;
+  ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh0) * a.max_parts + part;
   ro.prow_step = a.max_parts;
-  decode_range<D, T, NW>(a, smem, seq, kvh, L, a.new_k != nullptr && Lorig == L, t0, t1, ro,
-                         false);
+  decode_range<D, T, NW>(a, smem, seq, kvh, qh0, nh, L,
+                         a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro, false);
 }
 
 // Balanced split: the tiles of all sequences (for one kv head) are laid end
@@ -441,9 +453,10 @@ paged_decode_kernel(DecodeArgs a) {
 // the same prefix sums of tiles per sequence from seq_lens, so the split
 // follows the actual lengths without a host round trip.  A sequence inside
 // one workgroup's range is finished there; the pieces of a sequence that
-// crosses ranges go to workspace rows (kvh*(gridDim.x + num_seqs) + c + seq)*G
-// + h -- distinct for distinct (c, seq) because the ranges and the sequences
-// are both in increasing order -- and the merge kernel combines them.
+// crosses ranges go to workspace rows (y*(gridDim.x + num_seqs) + c + seq)*Gc
+// + h, y = blockIdx.y (kv head x head chunk) -- distinct for distinct (c, seq)
+// because the ranges and the sequences are both in increasing order -- and
+// the merge kernel combines them.
 constexpr int kBalMinTiles = 4 * kWaves;
 
 __device__ __forceinline__ int tiles_of(const DecodeArgs& a, int seq) {
@@ -482,13 +495,15 @@ template <int D, typename T, int NW>
 __global__ void __launch_bounds__(NW* kWave)
 paged_decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int c = blockIdx.x, kvh = blockIdx.y, nc = gridDim.x;
-  const int B = a.num_seqs, G = a.G;
+  const int c = blockIdx.x, y = blockIdx.y, nc = gridDim.x;
+  const int kvh = y / a.chunks, hc = y % a.chunks;
+  const int qh0 = kvh * a.G + hc * a.Gc, nh = min(a.Gc, a.G - hc * a.Gc);
+  const int B = a.num_seqs;
   int* starts = reinterpret_cast<int*>(smem + a.lds_main);
   tile_prefix(a, starts, starts + B + 1);
   const int total = starts[B];
   const int per = max((total + nc - 1) / nc, kBalMinTiles);
-  if (c == 0 && kvh == 0) {
+  if (c == 0 && y == 0) {
     // Split geometry for the merge kernel.
     if (threadIdx.x == 0) a.ws_hdr[0] = per;
     for (int s = threadIdx.x; s <= B; s += blockDim.x) a.ws_hdr[1 + s] = starts[s];
@@ -509,11 +524,12 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     const int t0 = pos - s0, t1 = min(r1, s1) - s0;
     RangeOut ro;
     ro.whole = (t0 == 0 && t1 == s1 - s0);
-    ro.prow0 = (static_cast<int64_t>(kvh) * (nc + B) + c + seq) * G;
+    ro.prow0 = (static_cast<int64_t>(y) * (nc + B) + c + seq) * a.Gc;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T, NW>(a, smem, seq, kvh, L, a.new_k != nullptr && a.seq_lens[seq] == L, t0,
-                           t1, ro, true);
+    decode_range<D, T, NW>(a, smem, seq, kvh, qh0, nh, L,
+                           a.new_k != nullptr && a.seq_lens[seq] == L, hc == 0, t0, t1, ro,
+                           true);
     pos = s0 + t1;
   }
 }
@@ -545,7 +561,7 @@ template <int D, typename T>
 __global__ void __launch_bounds__(D)
 paged_decode_merge_balanced_kernel(DecodeArgs a) {
   const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
-  const int G = a.G, B = a.num_seqs, nc = a.max_parts;
+  const int B = a.num_seqs, nc = a.max_parts;
   const int L = clamped_len(a, seq);
   if (L <= 0) {
     a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(0.f);  // zero bits in either type
@@ -554,12 +570,12 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
   const int per = a.ws_hdr[0];
   const int c0 = a.ws_hdr[1 + seq] / per, c1 = (a.ws_hdr[2 + seq] - 1) / per;
   if (c0 == c1) return;
-  const int kvh = qh / G, h = qh % G;
-  const int64_t base = static_cast<int64_t>(kvh) * (nc + B) + seq;
+  const int hg = qh % a.G, y = (qh / a.G) * a.chunks + hg / a.Gc, h = hg % a.Gc;
+  const int64_t base = static_cast<int64_t>(y) * (nc + B) + seq;
   MergeAcc m;
 #pragma unroll 4
   for (int c = c0; c <= c1; ++c) {
-    const int64_t row = (base + c) * G + h;
+    const int64_t row = (base + c) * a.Gc + h;
     m.add(a.ws_ml[row * 2], a.ws_ml[row * 2 + 1], a.ws_acc[row * D + d]);
   }
   reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(m.value());
@@ -601,20 +617,75 @@ paged_decode_merge_kernel(DecodeArgs a) {
   reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(t.value());
 }
 
-int g_num_cus = 0;
+// Merge of caller-supplied attention states (vaa_merge_attn_states): row
+// (s, h) combines partial outputs o_p (normalised, fp32) with their
+// log-sum-exps lse_p (natural log of the partition's softmax denominator),
+//   out = sum_p e^(lse_p - LSE) o_p,  LSE = log sum_p e^(lse_p),
+// through MergeAcc in the log2 domain (m_p = lse_p log2 e, l_p = 1).
+// Partitions with lse_p = -inf (or NaN) hold no keys and are skipped; a row
+// with none is zero, and its merged lse -inf.
+struct StatesArgs {
+  const float* part_out;   // [S, H, P, D]
+  const float* part_lse;   // [S, H, P]
+  const int32_t* num_parts;  // [S] or null (all P)
+  f16* out;
+  float* out_lse;          // [S, H] or null
+  int H, P, D;
+  int64_t o_st, o_sh;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(128) merge_states_kernel(StatesArgs a) {
+  const int h = blockIdx.x, s = blockIdx.y;
+  int n = a.P;
+  if (a.num_parts) n = min(max(a.num_parts[s], 0), a.P);
+  const int64_t row0 = (static_cast<int64_t>(s) * a.H + h) * a.P;
+  for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+    MergeAcc m;
+    for (int p = 0; p < n; ++p) {
+      const float lse = a.part_lse[row0 + p];
+      const bool has = lse > -INFINITY;  // false for -inf and NaN
+      m.add(has ? lse * kLog2e : 0.f, has ? 1.f : 0.f, a.part_out[(row0 + p) * a.D + d]);
+    }
+    reinterpret_cast<T*>(a.out)[s * a.o_st + h * a.o_sh + d] = Elem<T>::from_f(m.value());
+    if (a.out_lse && d == 0)
+      a.out_lse[static_cast<int64_t>(s) * a.H + h] =
+          m.den > 0.f ? (m.M + __builtin_log2f(m.den)) * (1.f / kLog2e) : -INFINITY;
+  }
+}
+
+// Compute units of the current device, queried once per device.  Each
+// entry is written with the same value by whichever thread gets there first
+// (a relaxed atomic: concurrent first calls only repeat the query).
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_num_cus[kMaxDevices];
 
 int num_cus() {
-  if (g_num_cus > 0) return g_num_cus;
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int n = g_num_cus[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+  }
+  int n = 0;
+  if (dev < 0 ||
       hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       n <= 0)
     n = 256;
-  g_num_cus = n;
+  if (dev >= 0 && dev < kMaxDevices) g_num_cus[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
 constexpr int kBalMaxSeqs = 8192;  // prefix sums of tiles per sequence live in LDS
+constexpr int kMaxGroupCols = 16;  // query heads per workgroup: the MFMA's 16 columns
+
+// A GQA group of G query heads is served in ceil(G/16) chunks of
+// ceil(G/chunks) heads (the last one may hold fewer), one workgroup each.
+inline int head_chunks(int G) { return (G + kMaxGroupCols - 1) / kMaxGroupCols; }
+inline int heads_per_chunk(int G) {
+  const int c = head_chunks(G);
+  return (G + c - 1) / c;
+}
 
 // How a call splits its sequences.
 struct Split {
@@ -622,6 +693,7 @@ struct Split {
   bool shared;       // balanced over 4-wave workgroups, two per CU
   int part;          // fixed: tokens per partition (balanced: -1)
   int max_parts;     // fixed: partitions per sequence; balanced: workgroups per kv head
+                     // and head chunk
   size_t ws_bytes;   // workspace needed (0: none)
   size_t hdr_bytes;  // balanced: bytes before the partial rows
 };
@@ -647,14 +719,15 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
                   kBalMaxSeqs);
     const bool shared = part == VAA_PARTITION_BALANCED_SHARED;
     const int per_cu = shared ? kWaves / kSharedWaves : 1;
-    const int wgs = (per_cu * num_cus() + p->num_kv_heads - 1) / p->num_kv_heads;
+    const int ys = p->num_kv_heads * head_chunks(p->queries_per_kv);
+    const int wgs = (per_cu * num_cus() + ys - 1) / ys;
     sp->balanced = true;
     sp->shared = shared;
     sp->part = static_cast<int>(part);
     sp->max_parts = wgs < 1 ? 1 : wgs;
     sp->hdr_bytes = ((static_cast<size_t>(p->num_seqs) + 2) * sizeof(int) + 255) / 256 * 256;
-    const size_t rows = static_cast<size_t>(p->num_kv_heads) * (sp->max_parts + p->num_seqs) *
-                        p->queries_per_kv;
+    const size_t rows = static_cast<size_t>(ys) * (sp->max_parts + p->num_seqs) *
+                        heads_per_chunk(p->queries_per_kv);
     sp->ws_bytes = sp->hdr_bytes + rows * row_bytes;
     return VAA_OK;
   }
@@ -664,7 +737,8 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
                   "partition_size=%lld must be a positive multiple of %d",
                   (long long)part, quantum);
   } else if (part == 0) {
-    const int64_t pairs = static_cast<int64_t>(p->num_seqs) * p->num_kv_heads;
+    const int64_t pairs = static_cast<int64_t>(p->num_seqs) * p->num_kv_heads *
+                          head_chunks(p->queries_per_kv);
     int64_t splits = pairs > 0 ? (num_cus() + pairs - 1) / pairs : 1;
     if (splits < 1) splits = 1;
     part = (max_len + splits - 1) / splits;
@@ -702,9 +776,6 @@ int check_params(const vaa_attn_params* p, const char* what) {
   if (!valid_dtype(p->dtype))
     return fail(VAA_ERR_UNSUPPORTED, "%s: dtype=%d (VAA_DTYPE_F16 or VAA_DTYPE_BF16)", what,
                 p->dtype);
-  if (p->queries_per_kv > 16)
-    return fail(VAA_ERR_UNSUPPORTED, "%s: queries_per_kv=%d > 16", what,
-                p->queries_per_kv);
   if (p->num_seqs < 0 || p->max_blocks_per_seq <= 0 || p->num_blocks <= 0)
     return fail(VAA_ERR_INVALID_ARG,
                 "%s: num_seqs=%d max_blocks_per_seq=%d num_blocks=%lld", what,
@@ -729,34 +800,35 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
   DecodeArgs a = a0;
   const size_t lds_tiles = static_cast<size_t>(kWaves) * kTile * D * sizeof(f16);
   const size_t lds_comb =
-      (2 * kWaves * 16 + static_cast<size_t>(kWaves) * a.G * D) * sizeof(float);
+      (2 * kWaves * 16 + static_cast<size_t>(kWaves) * a.Gc * D) * sizeof(float);
   const size_t lds = lds_tiles > lds_comb ? lds_tiles : lds_comb;
   if (balanced) {
     const int nw = shared ? kSharedWaves : kWaves;
     const size_t lds_bal =
         std::max(static_cast<size_t>(nw) * kTile * D * sizeof(f16),
-                 (2 * nw * 16 + static_cast<size_t>(nw) * a.G * D) * sizeof(float));
+                 (2 * nw * 16 + static_cast<size_t>(nw) * a.Gc * D) * sizeof(float));
     a.lds_main = static_cast<int>((lds_bal + 15) / 16 * 16);
     const size_t lds_b = a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kWaves) * sizeof(int);
     if (shared)
       hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kSharedWaves>),
-                         dim3(a.max_parts, a.num_kv_heads), dim3(kSharedWaves * kWave), lds_b,
+                         dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kSharedWaves * kWave),
+                         lds_b,
                          stream, a);
     else
       hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kWaves>),
-                         dim3(a.max_parts, a.num_kv_heads), dim3(kWaves * kWave), lds_b, stream,
-                         a);
+                         dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kWaves * kWave), lds_b,
+                         stream, a);
     int st = check_launch("paged_decode_balanced_kernel");
     if (st) return st;
     hipLaunchKernelGGL((paged_decode_merge_balanced_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs),
                        dim3(D), 0, stream, a);
     return check_launch("paged_decode_merge_balanced_kernel");
   }
-  dim3 grid(a.max_parts, a.num_kv_heads, a.num_seqs);
+  dim3 grid(a.max_parts, a.num_kv_heads * a.chunks, a.num_seqs);
   if (a.max_parts > 1 && a.part_tiles <= kShortPartTiles) {
     constexpr int kNw = kWaves / 2;
     const size_t lds4 = std::max(static_cast<size_t>(kNw) * kTile * D * sizeof(f16),
-                                 (2 * kNw * 16 + static_cast<size_t>(kNw) * a.G * D) *
+                                 (2 * kNw * 16 + static_cast<size_t>(kNw) * a.Gc * D) *
                                      sizeof(float));
     hipLaunchKernelGGL((paged_decode_kernel<D, T, kNw>), grid, dim3(kNw * kWave), lds4, stream,
                        a);
@@ -850,6 +922,8 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   a.num_kv_heads = p->num_kv_heads;
   a.num_q_heads = p->num_query_heads;
   a.G = p->queries_per_kv;
+  a.chunks = head_chunks(a.G);
+  a.Gc = heads_per_chunk(a.G);
   a.part_tiles = sp.balanced ? 0 : sp.part / kTile;
   a.max_parts = sp.max_parts;
   a.lds_main = 0;
@@ -873,4 +947,40 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
                         : launch_decode<128, f16>(a, sp.balanced, sp.shared, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
+}
+
+extern "C" int vaa_merge_attn_states(const float* partial_out, const float* partial_lse,
+                                     const int32_t* num_parts, int num_seqs, int num_heads,
+                                     int max_parts, int head_size, uint16_t* output,
+                                     int64_t o_stride_token, int64_t o_stride_head,
+                                     float* output_lse, int dtype, void* stream) {
+  if (num_seqs < 0 || num_heads <= 0 || max_parts <= 0 || head_size <= 0)
+    return fail(VAA_ERR_INVALID_ARG,
+                "vaa_merge_attn_states: num_seqs=%d num_heads=%d max_parts=%d head_size=%d",
+                num_seqs, num_heads, max_parts, head_size);
+  if (!valid_dtype(dtype))
+    return fail(VAA_ERR_UNSUPPORTED, "vaa_merge_attn_states: dtype=%d", dtype);
+  if (num_seqs == 0) return VAA_OK;
+  if (!partial_out || !partial_lse || !output)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_merge_attn_states: null pointer");
+  if (o_stride_token < 0 || o_stride_head < 0 || num_heads > 65535)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_merge_attn_states: bad output strides or heads");
+  StatesArgs a;
+  a.part_out = partial_out;
+  a.part_lse = partial_lse;
+  a.num_parts = num_parts;
+  a.out = reinterpret_cast<f16*>(output);
+  a.out_lse = output_lse;
+  a.H = num_heads;
+  a.P = max_parts;
+  a.D = head_size;
+  a.o_st = o_stride_token;
+  a.o_sh = o_stride_head;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == VAA_DTYPE_BF16)
+    hipLaunchKernelGGL((merge_states_kernel<bf16>), dim3(num_heads, num_seqs), dim3(128), 0, st,
+                       a);
+  else
+    hipLaunchKernelGGL((merge_states_kernel<f16>), dim3(num_heads, num_seqs), dim3(128), 0, st, a);
+  return check_launch("merge_states_kernel");
 }

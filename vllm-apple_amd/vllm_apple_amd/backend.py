@@ -212,21 +212,24 @@ class HipAttentionImpl(AttentionImpl):
         if alibi_slopes is not None:
             logger.warning("%s does not support ALiBi slopes, ignoring", BACKEND_NAME)
         self.alibi_slopes = None
-        if sliding_window is None:
-            self.sliding_window = (-1, -1)
-        elif attn_type == AttentionType.ENCODER_ONLY:
-            self.sliding_window = (sliding_window - 1, sliding_window - 1)
-        else:
-            self.sliding_window = (sliding_window - 1, 0)
+        # The kernels attend over the whole context.  The reference keeps the
+        # window and ignores it (metal_attn.py:377-382); a layer with a window
+        # (Mistral-7B-v0.1, Gemma-2/3, Qwen2 SWA layers) would then silently
+        # attend too far, so it is refused here instead.
+        if sliding_window is not None:
+            raise NotImplementedError(
+                f"sliding_window={sliding_window} is not supported by {BACKEND_NAME}: "
+                "the kernels attend over the whole context")
+        self.sliding_window = (-1, -1)
         self.kv_cache_dtype = kv_cache_dtype
         self.num_queries_per_kv = num_heads // num_kv_heads
         if is_quantized_kv_cache(kv_cache_dtype):
             raise NotImplementedError(f"FP8 KV cache is unsupported in {BACKEND_NAME}")
         if head_size not in SUPPORTED_HEAD_SIZES:
             raise ValueError(f"head_size must be 32/64/96/128, got {head_size}")
-        if num_heads % num_kv_heads != 0 or self.num_queries_per_kv > 16:
-            raise NotImplementedError(
-                f"num_heads={num_heads}, num_kv_heads={num_kv_heads}: GQA groups up to 16")
+        if num_heads % num_kv_heads != 0:
+            raise ValueError(
+                f"num_heads={num_heads} is not a multiple of num_kv_heads={num_kv_heads}")
         self.attn_type = attn_type
         self.sinks = sinks
         self._shadow: Optional[torch.Tensor] = None

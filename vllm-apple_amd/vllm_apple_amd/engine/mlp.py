@@ -46,6 +46,7 @@ class EngineMLP:
         self._down_proj = None
         self._fused_gate_up = False
         self._scratch: Optional[torch.Tensor] = None
+        self._scratch_streams: set = set()
 
     def set_weights(self, gate_proj: Optional[torch.Tensor] = None,
                     up_proj: Optional[torch.Tensor] = None,
@@ -72,11 +73,23 @@ class EngineMLP:
             return x
         return x, 0
 
-    def _intermediate(self, num_tokens: int, like: torch.Tensor) -> torch.Tensor:
+    def _intermediate(self, num_tokens: int, like: torch.Tensor,
+                      stream: torch.cuda.Stream) -> torch.Tensor:
+        """The activated [T, I] scratch, allocated on the stream that writes
+        and reads it, so that when it is outgrown the old block returns to
+        that stream's pool and is reused only by work ordered after the
+        kernels still using it.  A scratch first made on another stream is
+        marked as used on this one (record_stream) before it can be freed."""
         n = num_tokens * self.config.intermediate_size
         if (self._scratch is None or self._scratch.numel() < n
                 or self._scratch.dtype != like.dtype or self._scratch.device != like.device):
-            self._scratch = torch.empty(n, dtype=like.dtype, device=like.device)
+            self._scratch = None
+            with torch.cuda.stream(stream):
+                self._scratch = torch.empty(n, dtype=like.dtype, device=like.device)
+            self._scratch_streams = {stream.cuda_stream}
+        elif stream.cuda_stream not in self._scratch_streams:
+            self._scratch.record_stream(stream)
+            self._scratch_streams.add(stream.cuda_stream)
         return self._scratch[:n].view(num_tokens, self.config.intermediate_size)
 
     def encode(self, step_ctx: Any, hidden_states: Any, output_buffer: Any, num_tokens: int,
@@ -93,12 +106,12 @@ class EngineMLP:
         ob, oo = self._buf(output_buffer)
         x = view(hb, ho, (num_tokens, H), dtype=hb.dtype)
         out = view(ob, oo, (num_tokens, H), dtype=ob.dtype)
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
         if intermediate_buffer is not None:
             ib, io = self._buf(intermediate_buffer)
             act = view(ib, io, (num_tokens, I), dtype=ib.dtype)
         else:
-            act = self._intermediate(num_tokens, x)
-        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+            act = self._intermediate(num_tokens, x, s)
         with torch.cuda.stream(s):
             if self._fused_gate_up:
                 kernels.gate_up_silu(x, self._gate_up_proj, out=act, stream=s)

@@ -215,20 +215,44 @@ def _check_tables(block_table: torch.Tensor, seq_lens: torch.Tensor) -> None:
         raise ValueError("block_table has fewer rows than seq_lens")
 
 
-_workspaces: dict[int, torch.Tensor] = {}
 def _dev_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
+class _GrowOnlyScratch:
+    """One grow-only byte buffer per device, shared by calls ordered on one
+    stream.  A buffer that is outgrown is kept alive, never freed: a HIP
+    graph captured while it was current holds its address, and replaying
+    that graph must not write into memory the caching allocator has handed to
+    another tensor.  Sizes grow at least 2x, so the kept buffers sum to less
+    than the current one."""
+
+    def __init__(self, min_bytes: int = 1 << 20):
+        self._cur: dict[int, torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
+        self._min = min_bytes
+
+    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        idx = _dev_index(device)
+        ws = self._cur.get(idx)
+        if ws is None or ws.numel() < nbytes:
+            size = max(nbytes, self._min)
+            if ws is not None:
+                self._retired.append(ws)
+                size = max(size, 2 * ws.numel())
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            self._cur[idx] = ws
+        return ws
+
+
+_decode_ws = _GrowOnlyScratch()
+
+
 def decode_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     """Grow-only split-K scratch (partials) per device, reused across calls
-    that are ordered on one stream (torch's current stream by default)."""
-    idx = _dev_index(device)
-    ws = _workspaces.get(idx)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[idx] = ws
-    return ws
+    that are ordered on one stream (torch's current stream by default);
+    outgrown buffers stay allocated (graph replays may still use them)."""
+    return _decode_ws.get(nbytes, device)
 
 
 _side_streams: dict[int, torch.cuda.Stream] = {}
@@ -396,7 +420,11 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
         raise ValueError("new_keys and new_values must share strides")
     if partition_size == 0 and seq_lens_host is not None:
         kvh = key_cache.shape[1] if layout == "kernel" else key_cache.shape[2]
-        partition_size = choose_partition_size(seq_lens_host, kvh, device_cus(query.device))
+        # Groups of more than 16 query heads run one workgroup per chunk of
+        # at most 16 heads: the cost model counts those chunks as kv heads.
+        chunks = -(-(query.shape[1] // kvh) // 16)
+        partition_size = choose_partition_size(seq_lens_host, kvh * chunks,
+                                               device_cus(query.device))
         if shared and partition_size == PARTITION_BALANCED:
             partition_size = PARTITION_BALANCED_SHARED
     p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
@@ -417,6 +445,44 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
               key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
               seq_lens.data_ptr(), output.data_ptr(), _ptr(new_keys), _ptr(new_values),
               ws_ptr, ws_len, _lib.stream_handle(stream))
+    return output
+
+
+def merge_attn_states(partial_out: torch.Tensor, partial_lse: torch.Tensor, *,
+                      num_parts: torch.Tensor | None = None, output: torch.Tensor | None = None,
+                      output_lse: torch.Tensor | None = None, dtype: torch.dtype = torch.float16,
+                      stream=None) -> torch.Tensor:
+    """Log-sum-exp merge of attention states (vaa_merge_attn_states):
+    out[s, h] = sum_p e^(lse_p - LSE) o_p, LSE = log sum_p e^(lse_p).
+
+    partial_out fp32 [S, H, P, D] (normalised partial outputs), partial_lse
+    fp32 [S, H, P] (natural-log softmax denominators, -inf for an empty
+    partition), num_parts int32 [S] (the first num_parts[s] partitions count)
+    or None.  Returns output [S, H, D] in `dtype` (fp16 or bf16, or output's
+    type); output_lse fp32 [S, H] receives LSE when given."""
+    _require_gpu(partial_out, partial_lse, num_parts, output, output_lse)
+    if partial_out.dtype != torch.float32 or partial_out.dim() != 4 \
+            or not partial_out.is_contiguous():
+        raise ValueError("partial_out must be a contiguous fp32 [S, H, P, D] tensor")
+    S, H, P, D = partial_out.shape
+    if partial_lse.dtype != torch.float32 or tuple(partial_lse.shape) != (S, H, P) \
+            or not partial_lse.is_contiguous():
+        raise ValueError(f"partial_lse must be a contiguous fp32 [{S}, {H}, {P}] tensor")
+    if num_parts is not None and (num_parts.dtype != torch.int32 or num_parts.numel() < S
+                                  or not num_parts.is_contiguous()):
+        raise ValueError("num_parts must be a contiguous int32 [S] tensor")
+    if output is None:
+        output = torch.empty((S, H, D), dtype=dtype, device=partial_out.device)
+    if output.dim() != 3 or tuple(output.shape) != (S, H, D) or output.stride(2) != 1:
+        raise ValueError("output must be [S, H, D] with a contiguous last dim")
+    if output_lse is not None and (output_lse.dtype != torch.float32
+                                   or tuple(output_lse.shape) != (S, H)
+                                   or not output_lse.is_contiguous()):
+        raise ValueError("output_lse must be a contiguous fp32 [S, H] tensor")
+    _lib.call("vaa_merge_attn_states", partial_out.data_ptr(), partial_lse.data_ptr(),
+              _ptr(num_parts), S, H, P, D, output.data_ptr(), output.stride(0), output.stride(1),
+              _ptr(output_lse), ATTN_DTYPES[_attn_dtype(output=output)],
+              _lib.stream_handle(stream))
     return output
 
 
@@ -640,7 +706,7 @@ def qkv_epilogue(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
 TOPK_MAX_K = 256
 
 
-_topk_workspaces: dict[int, torch.Tensor] = {}
+_topk_ws = _GrowOnlyScratch()
 
 
 def topk_workspace_size(num_tokens: int, vocab_size: int, k: int) -> int:
@@ -676,12 +742,7 @@ def topk_logits(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = 
         raise ValueError("indices/values must be [T, k] (int32 / the logits' type), same strides")
     nbytes = topk_workspace_size(T, V, k)
     if workspace is None and nbytes > 0:
-        idx = _dev_index(logits.device)
-        workspace = _topk_workspaces.get(idx)
-        if workspace is None or workspace.numel() < nbytes:
-            workspace = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8,
-                                    device=logits.device)
-            _topk_workspaces[idx] = workspace
+        workspace = _topk_ws.get(nbytes, logits.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _lib.call("vaa_topk_logits", logits.data_ptr(), T, V, logits.stride(0), k,

@@ -51,17 +51,20 @@ class KVCacheDescriptor:
 
     @property
     def block_size_bytes(self) -> int:
-        """Size of one cache block in bytes (K + V)."""
-        element_size = 2 if self.dtype == torch.float16 else 4
-        return self.num_kv_heads * self.block_size * self.head_size * element_size * 2
+        """Bytes of one block of one layer, K and V together: two
+        [KV, bs, D] tiles of the cache's element type (2 bytes for fp16 and
+        bf16 alike)."""
+        elems = self.num_kv_heads * self.block_size * self.head_size
+        return 2 * elems * torch.empty((), dtype=self.dtype).element_size()
 
     @property
     def total_cache_bytes(self) -> int:
-        return self.block_size_bytes * self.num_blocks * self.num_layers
+        """Bytes of the whole cache: every block of every layer."""
+        return self.num_layers * self.num_blocks * self.block_size_bytes
 
     @property
     def total_cache_mb(self) -> float:
-        return self.total_cache_bytes / (1024 * 1024)
+        return self.total_cache_bytes / float(1 << 20)
 
 
 def _to_host(x: Union[np.ndarray, torch.Tensor]) -> np.ndarray:
@@ -182,8 +185,8 @@ class HipKVCache:
             raise ValueError(f"token_offset {token_offset} >= block_size {self._desc.block_size}")
         k, v = self.get_buffers(layer_idx)
         dev = k.device
-        key = torch.as_tensor(key).to(device=dev, dtype=torch.float16).contiguous()
-        value = torch.as_tensor(value).to(device=dev, dtype=torch.float16).contiguous()
+        key = torch.as_tensor(key).to(device=dev, dtype=k.dtype).contiguous()
+        value = torch.as_tensor(value).to(device=dev, dtype=k.dtype).contiguous()
         kernels.write_kv_single(k, v, key, value, block_id, token_offset, self._strides["block"],
                                 self._strides["head"], self._strides["token"],
                                 self._desc.num_blocks)
