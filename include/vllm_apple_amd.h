@@ -209,6 +209,28 @@ int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
                                size_t workspace_bytes, void* stream);
 
 /*
+ * vaa_paged_attention_decode without a workspace argument: it allocates
+ * nothing and takes no caller memory beyond its inputs and outputs.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * vaa_paged_attention_decode otherwise.  The split-K partials go to a fixed
+ * device array of vaa_paged_attention_decode_noalloc_max_workspace() bytes
+ * (32 MiB), one per GPU, held until the process ends; a split that needs
+ * more (vaa_paged_attention_decode_workspace_size) is refused with
+ * VAA_ERR_WORKSPACE before anything is enqueued.  The stream must belong to
+ * the current device.  All calls on one GPU share its array: calls that can
+ * overlap on one GPU (different streams, no ordering) race and must not be
+ * made.
+ */
+size_t vaa_paged_attention_decode_noalloc_max_workspace(void);
+int vaa_paged_attention_decode_noalloc(const vaa_attn_params* p, const uint16_t* query,
+                                       uint16_t* key_cache, uint16_t* value_cache,
+                                       const int32_t* block_table, const int32_t* seq_lens,
+                                       uint16_t* output, const uint16_t* new_keys,
+                                       const uint16_t* new_values, void* stream);
+
+/*
  * Merge of attention states: the split-K second pass on its own, for partial
  * results the caller computed (partitions of one context decoded apart, a
  * context split across GPUs, a shared prefix and a per-request suffix).  No

@@ -859,32 +859,31 @@ extern "C" size_t vaa_paged_attention_decode_workspace_size(const vaa_attn_param
   return sp.ws_bytes;
 }
 
-extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
-                                          const uint16_t* query,
-                                          uint16_t* key_cache,
-                                          uint16_t* value_cache,
-                                          const int32_t* block_table,
-                                          const int32_t* seq_lens,
-                                          uint16_t* output,
-                                          const uint16_t* new_keys,
-                                          const uint16_t* new_values,
-                                          void* workspace, size_t workspace_bytes,
-                                          void* stream) {
-  int st = check_params(p, "vaa_paged_attention_decode");
+namespace vaa {
+namespace {
+
+// The body of vaa_paged_attention_decode, given the workspace; `what` names
+// the entry point in error messages.
+int decode_impl(const char* what, const vaa_attn_params* p, const uint16_t* query,
+                uint16_t* key_cache, uint16_t* value_cache, const int32_t* block_table,
+                const int32_t* seq_lens, uint16_t* output, const uint16_t* new_keys,
+                const uint16_t* new_values, void* workspace, size_t workspace_bytes,
+                void* stream) {
+  int st = check_params(p, what);
   if (st) return st;
   if (p->num_seqs == 0) return VAA_OK;
   if (!query || !key_cache || !value_cache || !block_table || !seq_lens || !output)
-    return fail(VAA_ERR_INVALID_ARG, "vaa_paged_attention_decode: null pointer");
+    return fail(VAA_ERR_INVALID_ARG, "%s: null pointer", what);
   if ((new_keys == nullptr) != (new_values == nullptr))
     return fail(VAA_ERR_INVALID_ARG,
-                "vaa_paged_attention_decode: new_keys and new_values go together");
+                "%s: new_keys and new_values go together", what);
   if (new_keys && (p->new_kv_stride_token % 8 || p->new_kv_stride_head % 8 ||
                    !aligned16(new_keys) || !aligned16(new_values)))
     return fail(VAA_ERR_INVALID_ARG,
-                "vaa_paged_attention_decode: new K/V must be 16-byte aligned rows");
+                "%s: new K/V must be 16-byte aligned rows", what);
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache))
     return fail(VAA_ERR_INVALID_ARG,
-                "vaa_paged_attention_decode: query and caches must be 16-byte aligned");
+                "%s: query and caches must be 16-byte aligned", what);
   Split sp;
   st = plan_split(p, &sp);
   if (st) return st;
@@ -904,11 +903,11 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
   if (sp.ws_bytes > 0) {
     if (!workspace || workspace_bytes < sp.ws_bytes)
       return fail(VAA_ERR_WORKSPACE,
-                  "vaa_paged_attention_decode: workspace %zu bytes < %zu needed",
-                  workspace_bytes, sp.ws_bytes);
+                  "%s: workspace %zu bytes < %zu needed", what, workspace_bytes,
+                  sp.ws_bytes);
     if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
       return fail(VAA_ERR_INVALID_ARG,
-                  "vaa_paged_attention_decode: workspace must be 16-byte aligned");
+                  "%s: workspace must be 16-byte aligned", what);
     const size_t rows = (sp.ws_bytes - sp.hdr_bytes) / ((p->head_size + 2) * sizeof(float));
     unsigned char* base = static_cast<unsigned char*>(workspace);
     a.ws_hdr = reinterpret_cast<int*>(base);
@@ -947,6 +946,93 @@ extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p,
                         : launch_decode<128, f16>(a, sp.balanced, sp.shared, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
+}
+
+}  // namespace
+}  // namespace vaa
+
+extern "C" int vaa_paged_attention_decode(const vaa_attn_params* p, const uint16_t* query,
+                                          uint16_t* key_cache, uint16_t* value_cache,
+                                          const int32_t* block_table, const int32_t* seq_lens,
+                                          uint16_t* output, const uint16_t* new_keys,
+                                          const uint16_t* new_values, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  return decode_impl("vaa_paged_attention_decode", p, query, key_cache, value_cache, block_table,
+                     seq_lens, output, new_keys, new_values, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode.  The split-K partials live in a fixed device array
+// instead of a caller workspace.  Each GPU the library runs on holds its own
+// copy of the array (kScratchBytes) until the process ends.  In host code
+// `scratch` names a host-side stand-in, not device memory: the kernels get
+// the device address from hipGetSymbolAddress, taken once per device on the
+// entry point's first call there with that device current.  The kernels
+// write every row and header word they read in the same call (the partials
+// of each split sequence, the balanced split's geometry), so nothing needs
+// clearing between calls.  Calls that overlap on one GPU share the array and
+// race.
+constexpr size_t kScratchBytes = size_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace vaa {
+namespace {
+
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of this device's copy of `scratch`, or null with the error
+// set.
+void* scratch_ptr(const char* what) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(VAA_ERR_HIP, "%s: no current HIP device (or device id >= %d)", what, kMaxDevices);
+    return nullptr;
+  }
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr) return ptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr) {
+    fail(VAA_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed: %s", what, hipGetErrorString(e));
+    return nullptr;
+  }
+  g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  return ptr;
+}
+
+}  // namespace
+}  // namespace vaa
+
+extern "C" size_t vaa_paged_attention_decode_noalloc_max_workspace(void) {
+  return kScratchBytes;
+}
+
+extern "C" int vaa_paged_attention_decode_noalloc(const vaa_attn_params* p,
+                                                  const uint16_t* query, uint16_t* key_cache,
+                                                  uint16_t* value_cache,
+                                                  const int32_t* block_table,
+                                                  const int32_t* seq_lens, uint16_t* output,
+                                                  const uint16_t* new_keys,
+                                                  const uint16_t* new_values, void* stream) {
+  const char* what = "vaa_paged_attention_decode_noalloc";
+  int st = check_params(p, what);
+  if (st) return st;
+  if (p->num_seqs == 0) return VAA_OK;
+  Split sp;
+  st = plan_split(p, &sp);
+  if (st) return st;
+  if (sp.ws_bytes > kScratchBytes)
+    return fail(VAA_ERR_WORKSPACE,
+                "%s: this split needs %zu bytes of partials, above the fixed %zu-byte device "
+                "array (use VAA_PARTITION_BALANCED, larger partitions, or "
+                "vaa_paged_attention_decode with a workspace)",
+                what, sp.ws_bytes, kScratchBytes);
+  void* ws = nullptr;
+  if (sp.ws_bytes > 0) {
+    ws = scratch_ptr(what);
+    if (!ws) return VAA_ERR_HIP;
+  }
+  return decode_impl(what, p, query, key_cache, value_cache, block_table, seq_lens, output,
+                     new_keys, new_values, ws, sp.ws_bytes > 0 ? kScratchBytes : 0, stream);
 }
 
 extern "C" int vaa_merge_attn_states(const float* partial_out, const float* partial_lse,
