@@ -88,6 +88,16 @@ __device__ __forceinline__ int swz(int row) {
   else return (row >> 1) & 3;
 }
 
+// K tiles at D = 128: the chunk XOR takes all 16 values over 16 consecutive
+// rows, so a ds_read_b128 of one logical chunk down 16 rows hits 16 distinct
+// chunk slots (measured 201 against 121 B/clk per CU with the 8-value XOR).
+// V keeps swz, which the transposed reads need.
+template <int D>
+__device__ __forceinline__ int swzk(int row) {
+  if constexpr (D == 128) return row & 15;
+  else return swz<D>(row);
+}
+
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
@@ -168,13 +178,14 @@ __device__ __forceinline__ void lanes_init(const PrefillArgs& a, int wave, int l
   for (int q = 0; q < C::NI; ++q) {
     const int P = 64 * (wave * C::NI + q) + lane;  // chunk slot in the tile
     const int R = P / C::CH;                         // tile row (16*wave .. +15)
-    const int lc = (P % C::CH) ^ swz<D>(R);          // logical chunk stored there
+    const int lck = (P % C::CH) ^ swzk<D>(R);        // logical chunks stored there
+    const int lcv = (P % C::CH) ^ swz<D>(R);
     L.row[q] = R & 15;
-    L.koff[q] = static_cast<uint32_t>((R & 15) * a.k_st * 2 + lc * 16);
-    L.voff[q] = static_cast<uint32_t>((R & 15) * a.v_st * 2 + lc * 16);
+    L.koff[q] = static_cast<uint32_t>((R & 15) * a.k_st * 2 + lck * 16);
+    L.voff[q] = static_cast<uint32_t>((R & 15) * a.v_st * 2 + lcv * 16);
   }
   const int qj = lane & 31, hb = lane >> 5;
-  const int sk = swz<D>(qj);
+  const int sk = swzk<D>(qj);
 #pragma unroll
   for (int s2 = 0; s2 < C::NK; ++s2)
     L.kaddr[s2] = qj * C::ROWB + ((hb * (C::CH / 2) + s2) ^ sk) * 16;
@@ -261,32 +272,59 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
 
 // One 64-key tile for this wave's 32 query rows: S^T = K Q^T as two
 // independent 32-key MFMA row blocks, online softmax over both, then
-// O^T += V^T P^T over four 16-key groups.
+// O^T += V^T P^T over four 16-key groups.  The LDS operand reads run ahead
+// of their MFMAs (kKAhead K reads, kVAhead V^T pairs; the first V^T pairs are
+// issued before the softmax, whose VALU work then hides their latency), and
+// scheduling barriers keep the compiler from hoisting every read (which
+// would not fit the register budget of two waves per SIMD).
+constexpr int kKAhead = 4;
+constexpr int kVAhead = 4;
+
 template <int D, typename T>
 __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, const f16* vt,
                                           int key0, int lim, int hb, const Lanes<D>& L,
                                           const u32x4 (&qb)[PCfg<D>::NK], float& m_run,
                                           float& l_part, f32x16 (&acc)[PCfg<D>::NDT]) {
   using C = PCfg<D>;
+  using X4 = typename Elem<T>::x4;
+  using X8 = typename Elem<T>::x8;
+  constexpr int NKR = 2 * C::NK;   // K operand reads (b128)
+  constexpr int NPV = C::NDT * 4;  // PV MFMAs, one V^T pair each
   const char* kbytes = reinterpret_cast<const char*>(kt);
   const char* vbytes = reinterpret_cast<const char*>(vt);
-  // S^T block j: A lane = K[32j + l%32][hb*D/2 + 8s .. +7].
+  // S^T block j: A lane = K[32j + l%32][hb*D/2 + 8s .. +7]; read i covers
+  // step i/2 of block i%2.
+  u32x4 kA[NKR];
+  auto kread = [&](int i) {
+    kA[i] = *reinterpret_cast<const u32x4*>(kbytes + L.kaddr[i >> 1] + 32 * (i & 1) * C::ROWB);
+  };
+#pragma unroll
+  for (int i = 0; i < kKAhead && i < NKR; ++i) kread(i);
+  __builtin_amdgcn_sched_barrier(0);
   f32x16 sacc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) sacc[j][r] = 0.f;
 #pragma unroll
-  for (int s2 = 0; s2 < C::NK; ++s2) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const u32x4 kA =
-          *reinterpret_cast<const u32x4*>(kbytes + L.kaddr[s2] + 32 * j * C::ROWB);
-      sacc[j] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, kA),
-                                      __builtin_bit_cast(typename Elem<T>::x8, qb[s2]),
-                                      sacc[j]);
-    }
+  for (int i = 0; i < NKR; ++i) {
+    if (i + kKAhead < NKR) kread(i + kKAhead);
+    sacc[i & 1] = Elem<T>::mfma32x32x16(__builtin_bit_cast(X8, kA[i]),
+                                        __builtin_bit_cast(X8, qb[i >> 1]), sacc[i & 1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  // V^T for MFMA i (key group i / NDT, dim tile i % NDT) from the
+  // transposing LDS read.
+  X4 vlo[NPV], vhi[NPV];
+  auto vread = [&](int i) {
+    const int g = i / C::NDT, dt = i % C::NDT;
+    const f16* vp = reinterpret_cast<const f16*>(vbytes + L.vaddr[dt] + 16 * g * C::ROWB);
+    vlo[i] = lds_tr4<T>(vp);
+    vhi[i] = lds_tr4<T>(vp + 8 * D);
+  };
+#pragma unroll
+  for (int i = 0; i < kVAhead && i < NPV; ++i) vread(i);
+  __builtin_amdgcn_sched_barrier(0);
   // Lane holds keys 32j + 8(r/4) + 4hb + r%4 for query qj.  The mask is only
   // evaluated when some row of the wave cannot see the whole tile.
   const int rel = lim - key0;
@@ -317,7 +355,7 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
   }
   const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
   // pb[g]: B operand for 16-key group g (keys 16g + 8(i/4) + 4hb + i%4).
-  typename Elem<T>::x8 pb[4];
+  X8 pb[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -326,17 +364,16 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
       pb[2 * j + (r >> 3)][r & 7] = Elem<T>::from_f(p);
       l_part += p;
     }
-  // O^T += V^T P^T; V^T for key group g comes from the transposing LDS read.
+  __builtin_amdgcn_sched_barrier(0);
+  // O^T += V^T P^T.
 #pragma unroll
-  for (int dt = 0; dt < C::NDT; ++dt) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f16* vp = reinterpret_cast<const f16*>(vbytes + L.vaddr[dt] + 16 * g * C::ROWB);
-      const typename Elem<T>::x4 lo = lds_tr4<T>(vp);
-      const typename Elem<T>::x4 hi = lds_tr4<T>(vp + 8 * D);
-      const typename Elem<T>::x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      acc[dt] = Elem<T>::mfma32x32x16(va, pb[g], acc[dt]);
-    }
+  for (int i = 0; i < NPV; ++i) {
+    if (i + kVAhead < NPV) vread(i + kVAhead);
+    const int g = i / C::NDT, dt = i % C::NDT;
+    const X8 va = {vlo[i][0], vlo[i][1], vlo[i][2], vlo[i][3],
+                   vhi[i][0], vhi[i][1], vhi[i][2], vhi[i][3]};
+    acc[dt] = Elem<T>::mfma32x32x16(va, pb[g], acc[dt]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -356,12 +393,18 @@ paged_prefill_kernel(PrefillArgs a) {
   // XCD-aware placement: the hardware hands consecutive workgroup ids to the
   // 8 XCDs in turn, so id i runs on XCD i % 8.  Give each XCD a contiguous
   // range of (kv head, query tile) work so the query tiles that reuse one
-  // sequence's K/V tiles share that XCD's L2.
+  // sequence's K/V tiles share that XCD's L2.  The second half of an XCD's
+  // range is walked backwards: its workgroups take the CUs' second slots in
+  // dispatch order, so a CU pairs an early query tile of a chunk (short
+  // causal context) with a late one (long context) and the CUs finish
+  // together (C3: 6 % faster than pairing equal tiles).
   const int gx = gridDim.x;
   const int id = blockIdx.x + gx * blockIdx.y;
   if (id >= a.padded_tiles) return;  // grid rounding beyond the padded count
   const int per_xcd = a.padded_tiles / kXcds;
-  const int logical = (id % kXcds) * per_xcd + id / kXcds;
+  int kx = id / kXcds;
+  if (kx >= per_xcd / 2) kx = per_xcd - 1 - (kx - per_xcd / 2);
+  const int logical = (id % kXcds) * per_xcd + kx;
   if (logical >= gx * a.tiles_y) return;
   const int tile_x = logical % gx, tile_y = logical / gx;
   const int kvh = tile_y / a.head_chunks;
