@@ -92,51 +92,171 @@ def traffic_from_profile() -> float | None:
     return None
 
 
-def cpu_baseline(batch, budget_s: float) -> dict:
-    """Time the reference CPU torch path on a bounded sample of the same step."""
+def cpu_env() -> dict:
+    """The host the CPU baseline runs on.  Read before the GPU is touched
+    (`nproc` runs as a child process)."""
+    import subprocess
+
+    total = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = total
+    quota = None
+    try:  # cgroup v2 CPU quota: "<quota> <period>" or "max <period>"
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(q) // int(per))
+    except (OSError, ValueError):
+        pass
+    try:
+        nproc = int(subprocess.run(["nproc"], capture_output=True, text=True,
+                                   timeout=10).stdout.strip())
+    except (OSError, ValueError, subprocess.SubprocessError):
+        nproc = None
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     import torch
 
-    from oracle import ref_torch
+    return {"os_cpu_count": total, "affinity_cpus": affinity, "cgroup_cpus": quota,
+            "nproc": nproc, "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "cpu_model": model, "torch": torch.__version__,
+            # torch.set_num_threads(os.cpu_count()), capped at the CPUs this
+            # process may run on: threads beyond those only time-slice.
+            "threads": max(1, min(total, affinity, quota or total))}
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
-    # Sample: the first n sequences of the step, copied to host in the vLLM layout
-    # the reference torch path reads (conversion not timed).
-    n = min(4, batch.num_seqs)
-    bt = batch.block_table[:n].cpu()
-    nblk = (batch.extra["seq_lens_host"][0] + 15) // 16
-    used = bt[:, :nblk].reshape(-1).long()
-    kc = ref_torch.kernel_to_vllm_layout(batch.k_cache[used].cpu())
-    vc = ref_torch.kernel_to_vllm_layout(batch.v_cache[used].cpu())
-    local_bt = torch.arange(used.numel(), dtype=torch.int32).view(n, nblk)
-    q = batch.query[:n].cpu()
-    lens = batch.extra["seq_lens_host"][:n]
-    kv = batch.num_kv_heads
-    ref_torch.decode_sdpa(q, kc, vc, local_bt, lens, batch.scale, kv)  # warm-up
+
+_CPU_ENV: dict | None = None
+
+
+def _cpu_timed(fn, budget_s: float, min_runs: int = 5) -> tuple[float, int]:
+    """One warm-up call, then at least min_runs timed calls (more while the
+    budget lasts); returns (median seconds, runs)."""
+    fn()
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 1000):
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s
+                                    and len(times) < 200):
         t0 = time.perf_counter()
-        ref_torch.decode_sdpa(q, kc, vc, local_bt, lens, batch.scale, kv)
+        fn()
         times.append(time.perf_counter() - t0)
     times.sort()
-    med = times[len(times) // 2]
-    D, H = batch.head_size, batch.num_q_heads
-    sample_bytes = sum(lens) * kv * D * 2 * 2 + 2 * n * H * D * 2
-    return {
-        "value": round(sample_bytes / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"{n} of {batch.num_seqs} sequences (ctx {lens[0]}) of the same decode step, "
-                   f"reference torch path (mps_attn.py:284-357) on host, fp16 storage, "
-                   f"median of {len(times)} runs = {med * 1e3:.1f} ms "
-                   f"({n / med:.1f} tok/s); {torch.__version__}"),
-    }
+    return times[len(times) // 2], len(times)
+
+
+class HostStep:
+    """Host copies of a batch's sequences [0, n) in the vLLM layout the
+    reference's torch path reads ([nb, bs, KV, D], fp16 storage): only the
+    blocks those sequences use, renumbered, with their block table, slots and
+    tokens.  Building it is not timed."""
+
+    def __init__(self, b, n: int | None = None):
+        import torch
+
+        from oracle import ref_torch
+
+        S = b.num_seqs
+        n = S if n is None else min(n, S)
+        lens = b.extra["seq_lens_host"][:n]
+        bs = b.block_size
+        nblk = [(L + bs - 1) // bs for L in lens]
+        bt = b.block_table[:n].cpu()
+        used = torch.cat([bt[s, :k] for s, k in enumerate(nblk)]).long()
+        remap = torch.full((b.k_cache.shape[0],), -1, dtype=torch.int64)
+        remap[used] = torch.arange(used.numel())
+        self.k = ref_torch.kernel_to_vllm_layout(b.k_cache[used.to(b.k_cache.device)].cpu())
+        self.v = ref_torch.kernel_to_vllm_layout(b.v_cache[used.to(b.v_cache.device)].cpu())
+        self.bt = torch.full((n, max(nblk) if nblk else 1), -1, dtype=torch.int32)
+        for s, k in enumerate(nblk):
+            self.bt[s, :k] = remap[bt[s, :k].long()].to(torch.int32)
+        qsl = b.query_start_loc.cpu()
+        t1 = int(qsl[n])
+        self.q = b.query[:t1].cpu()
+        self.new_k, self.new_v = b.new_k[:t1].cpu(), b.new_v[:t1].cpu()
+        slots = b.slot_mapping[:t1].cpu()
+        self.slots = remap[slots // bs] * bs + slots % bs
+        self.qsl = qsl[:n + 1].tolist()
+        self.lens = list(lens)
+        self.n, self.num_tokens = n, t1
+        self.kv, self.scale = b.num_kv_heads, b.scale
+
+    def write(self):
+        from oracle import ref_torch
+
+        ref_torch.update_kv_cache_scatter(self.new_k, self.new_v, self.k, self.v, self.slots)
+
+    def decode(self, s0: int = 0, s1: int | None = None):
+        """Decode sequences [s0, s1) (one query token each)."""
+        from oracle import ref_torch
+
+        s1 = self.n if s1 is None else s1
+        t0, t1 = self.qsl[s0], self.qsl[s1]
+        return ref_torch.decode_sdpa(self.q[t0:t1], self.k, self.v, self.bt[s0:s1],
+                                     self.lens[s0:s1], self.scale, self.kv)
+
+    def prefill(self, s0: int = 0, s1: int | None = None):
+        """Chunked prefill of sequences [s0, s1) over their cached prefix."""
+        from oracle import ref_torch
+
+        s1 = self.n if s1 is None else s1
+        t0 = self.qsl[s0]
+        return ref_torch.prefill_sdpa_prefix(self.q[t0:self.qsl[s1]], self.k, self.v,
+                                             self.bt[s0:s1],
+                                             [x - t0 for x in self.qsl[s0:s1 + 1]],
+                                             self.lens[s0:s1], self.scale, self.kv)
+
+
+def cpu_record(value: float, unit: str, sample: str, **extra) -> dict:
+    env = _CPU_ENV or {}
+    rec = {"value": value, "unit": unit, "cores": env.get("threads"), "kind": "port",
+           "sample": sample}
+    rec.update(extra)
+    rec["host"] = {k: env.get(k) for k in ("cpu_model", "nproc", "os_cpu_count",
+                                           "affinity_cpus", "cgroup_cpus", "omp_num_threads",
+                                           "torch")}
+    return rec
+
+
+def _cpu_threads() -> int:
+    import torch
+
+    threads = (_CPU_ENV or {}).get("threads") or 1
+    torch.set_num_threads(threads)
+    return threads
+
+
+def cpu_decode_step(b, budget_s: float, n: int | None = None, what: str = "decode step") -> dict:
+    """The reference's CPU step for a decode batch: the KV scatter of the new
+    tokens (base_attn.py:308-342) then per-sequence gather + repeat_interleave
+    + SDPA (mps_attn.py:284-357), on sequences [0, n) of the batch."""
+    _cpu_threads()
+    h = HostStep(b, n)
+
+    def step():
+        h.write()
+        h.decode()
+
+    med, runs = _cpu_timed(step, budget_s)
+    lens = h.lens
+    B, H, KV, D = h.n, b.num_q_heads, b.num_kv_heads, b.head_size
+    alg = (sum(lens) * KV * D * 4 + 2 * B * H * D * 2 + 2 * 2 * B * KV * D * 2
+           + sum((L + b.block_size - 1) // b.block_size for L in lens) * 4 + B * 4)
+    sample = (f"{'all ' if h.n == b.num_seqs else ''}{h.n} of {b.num_seqs} sequences "
+              f"(ctx mean {sum(lens) / len(lens):.0f}, max {max(lens)}) of the same {what}, "
+              f"median of {runs} runs after 1 warm-up")
+    return cpu_record(round(alg / med / 1e9, 3), "GB/s", sample, ms_per_step=round(med * 1e3, 3),
+                      latency_us=round(med * 1e6, 1), tokens_per_s=round(h.n / med, 1),
+                      algorithmic_bytes=alg)
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
+
 
 
 def _timed(fn, steps: int, warmup: int) -> float:
@@ -249,6 +369,8 @@ def wl_c1(args) -> dict:
     b = workloads.c1_decode(device=torch.device("cuda:0"))
     r = _decode_record("C1", b, args, 0, "Qwen2-0.5B decode, B=4, cache-resident: latency")
     r["latency_us"] = round(r["ms_per_step"] * 1e3, 2)
+    if not args.no_cpu_baseline:
+        r["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds)
     return r
 
 
@@ -258,7 +380,10 @@ def wl_c2u(args) -> dict:
     from vllm_apple_amd import workloads
 
     b = workloads.c2_decode(device=torch.device("cuda:0"))
-    return _decode_record("C2u", b, args, 0, "ctx U{1024..8192}, split-K chosen from lengths")
+    r = _decode_record("C2u", b, args, 0, "ctx U{1024..8192}, split-K chosen from lengths")
+    if not args.no_cpu_baseline:
+        r["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds)
+    return r
 
 
 def wl_c4(args) -> dict:
@@ -272,6 +397,9 @@ def wl_c4(args) -> dict:
     r512["auto_partition"] = {k: rauto[k] for k in ("partition", "ms_per_step", "gb_s",
                                                    "pct_hbm_peak")}
     r512["scaled_key_rows"] = b.extra["scaled_rows"]
+    if not args.no_cpu_baseline:
+        # A quarter of the batch keeps the sample to a few seconds per step.
+        r512["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds, n=16)
     return r512
 
 
@@ -305,7 +433,7 @@ def wl_c3(args) -> dict:
     t_bf = _timed(lambda: kernels.paged_prefill(bb.query, bb.k_cache, bb.v_cache, bb.block_table,
                                                 bb.token_to_seq, bb.positions, scale=bb.scale,
                                                 output=out_b), args.steps, args.warmup)
-    return {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
+    rec = {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
             "tokens": T, "kv_write_ms": round(t_kv, 5),
             "kv_write_gb_s": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
             "prefill_ms": round(t_at, 5), "flops": fl,
@@ -313,6 +441,18 @@ def wl_c3(args) -> dict:
             "mfma_util_pct": round(100 * fl / (t_at * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2),
             "bf16_prefill_ms": round(t_bf, 5),
             "bf16_tflop_s": round(fl / (t_bf * 1e-3) / 1e12, 1)}
+    if not args.no_cpu_baseline:
+        _cpu_threads()
+        h = HostStep(b)
+        t_w, n_w = _cpu_timed(h.write, args.cpu_seconds / 3)
+        t_p, n_p = _cpu_timed(h.prefill, args.cpu_seconds * 2 / 3)
+        rec["cpu_baseline"] = cpu_record(
+            round(fl / t_p / 1e12, 4), "TFLOP/s",
+            f"the whole C3 step: KV scatter of {T} tokens (median of {n_w} runs) and the "
+            f"prefill of all 4 chunks over their prefixes (median of {n_p} runs), 1 warm-up each",
+            kv_write_ms=round(t_w * 1e3, 3), kv_write_gb_s=round(kv_bytes / t_w / 1e9, 3),
+            prefill_ms=round(t_p * 1e3, 3))
+    return rec
 
 
 def wl_c5(args) -> dict:
@@ -443,7 +583,52 @@ def wl_c5(args) -> dict:
                       ("add_rmsnorm", t_addnorm, addnorm_bytes)):
         rec[nm] = {"ms": round(t, 5), "bytes": by, "gb_s": round(by / (t * 1e-3) / 1e9, 1),
                    "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+    if not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_c5(b, args.cpu_seconds,
+                                     {"rmsnorm": norm_bytes, "rope": rope_bytes,
+                                      "silu_mul": silu_bytes})
     return rec
+
+
+def cpu_c5(b, budget_s: float, layer_bytes: dict) -> dict:
+    """The reference's CPU path for the whole C5 step: the KV scatter of all
+    2104 tokens, the 56 decodes, the 8 prefill chunks, then F.rms_norm over
+    the hidden rows, NeoX RoPE (runner.py:1500-1524) over q and k, and
+    F.silu(g) * u over the intermediate rows."""
+    import torch
+
+    import oracle.layer_ops as olo
+    from oracle import ref_torch
+
+    _cpu_threads()
+    h = HostStep(b)
+    nd = b.num_decode_tokens
+
+    def attn():
+        h.write()
+        h.decode(0, nd)
+        h.prefill(nd, h.n)
+
+    t_att, n_att = _cpu_timed(attn, budget_s)
+    x, w = b.extra["hidden"].cpu(), b.extra["norm_weight"].cpu()
+    eps = b.extra["eps"]
+    cos, sin = (torch.from_numpy(t) for t in olo.cos_sin(b.head_size, 16384,
+                                                          b.extra["rope_base"]))
+    pos = b.positions.cpu()
+    g, u = b.extra["gate"].cpu(), b.extra["up"].cpu()
+    parts = {}
+    for nm, fn in (("rmsnorm", lambda: ref_torch.rms_norm(x, w, eps)),
+                   ("rope", lambda: (ref_torch.rope_neox(h.q, pos, cos, sin),
+                                     ref_torch.rope_neox(h.new_k, pos, cos, sin))),
+                   ("silu_mul", lambda: ref_torch.silu_mul(g, u))):
+        t, n = _cpu_timed(fn, budget_s / 6)
+        parts[nm] = {"ms": round(t * 1e3, 3), "gb_s": round(layer_bytes[nm] / t / 1e9, 3),
+                     "runs": n}
+    return cpu_record(round(t_att * 1e3, 3), "ms per attention step",
+                      f"the whole C5 step: KV scatter of {h.num_tokens} tokens + {nd} decodes + "
+                      f"{h.n - nd} prefill chunks (median of {n_att} runs after 1 warm-up); "
+                      f"layer ops over all {h.num_tokens} tokens",
+                      layer_ops=parts)
 
 
 def wl_c2bf16(args) -> dict:
@@ -535,6 +720,9 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is described, not built)"}))
         return 2
+    global _CPU_ENV
+    if not args.no_cpu_baseline and not args.copy_bytes:
+        _CPU_ENV = cpu_env()
     import torch
 
     if args.copy_bytes:
@@ -645,7 +833,7 @@ def main() -> int:
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(b, args.cpu_seconds)
+        res["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds)
     print(json.dumps(res))
     return 0
 

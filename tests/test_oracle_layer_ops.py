@@ -204,3 +204,50 @@ def test_gate_up_silu_vs_matmul_and_special_cases():
     xs = rs.randn(2, H).astype(np.float16)
     assert not np.allclose(olo.gate_up_silu(xs, sq, sq.T.copy()),
                            olo.gate_up_silu(xs, sq, sq), rtol=1e-3)
+
+
+# -- the torch CPU path bench.py times as the CPU baseline (oracle/ref_torch.py) --------
+def test_ref_torch_layer_ops_vs_fp64_oracle():
+    """ref_torch.rms_norm / rope_neox / silu_mul compute in fp16 as the
+    reference's CPU path does; against the pinned fp64 oracle they stay
+    within fp16 rounding (the kernels' own tolerance, 2e-3 + 1e-2 |ref|)."""
+    import oracle.ref_torch as rt
+
+    rs = np.random.RandomState(8)
+    x = rs.randn(64, 5120).astype(np.float16)
+    w = (rs.randn(5120) * 0.1 + 1).astype(np.float16)
+    got = rt.rms_norm(torch.from_numpy(x), torch.from_numpy(w), 1e-6).double().numpy()
+    ref = olo.rms_norm(x, w, 1e-6)
+    assert np.all(np.abs(got - ref) <= 2e-3 + 1e-2 * np.abs(ref))
+
+    for D, base in ((128, 1e6), (64, 1e4)):
+        q = rs.randn(96, 8, D).astype(np.float16)
+        pos = rs.randint(0, 16384, size=96)
+        cos, sin = olo.cos_sin(D, 16384, base)
+        got = rt.rope_neox(torch.from_numpy(q), torch.from_numpy(pos), torch.from_numpy(cos),
+                           torch.from_numpy(sin)).double().numpy()
+        ref = olo.rope_neox(q, pos, cos, sin)
+        assert np.all(np.abs(got - ref) <= 2e-3 + 1e-2 * np.abs(ref)), D
+        # a plausible slip (halves swapped in the rotation) is far outside
+        t = torch.from_numpy(q).double()
+        c = torch.from_numpy(np.concatenate([cos, cos], -1))[torch.from_numpy(pos)].unsqueeze(1)
+        s = torch.from_numpy(np.concatenate([sin, sin], -1))[torch.from_numpy(pos)].unsqueeze(1)
+        slip = (t * c + torch.cat((t[..., D // 2:], -t[..., :D // 2]), -1) * s).numpy()
+        assert not np.all(np.abs(slip - ref) <= 2e-3 + 1e-2 * np.abs(ref))
+
+    g = (rs.randn(32, 1024) * 4).astype(np.float16)
+    u = rs.randn(32, 1024).astype(np.float16)
+    got = rt.silu_mul(torch.from_numpy(g), torch.from_numpy(u)).double().numpy()
+    ref = olo.silu_mul(g, u)
+    assert np.all(np.abs(got - ref) <= 2e-3 + 1e-2 * np.abs(ref))
+
+
+def test_ref_torch_layout_permute():
+    """kernel_to_vllm_layout: cache[b, h, t, d] lands at [b, t, h, d]."""
+    import oracle.ref_torch as rt
+
+    c = torch.arange(3 * 2 * 4 * 5, dtype=torch.float32).view(3, 2, 4, 5)
+    v = rt.kernel_to_vllm_layout(c)
+    assert v.shape == (3, 4, 2, 5) and v.is_contiguous()
+    for b, h, t, d in [(0, 0, 0, 0), (2, 1, 3, 4), (1, 0, 2, 3), (2, 1, 0, 1)]:
+        assert v[b, t, h, d] == c[b, h, t, d]
