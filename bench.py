@@ -47,7 +47,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C5mlp", "C2bf16", "topk",
-                             "all"],
+                             "C3-launches", "all"],
                     help="headline = the contract line; the others print one JSON line per "
                          "BASELINE config (measurement record, not the driver's metric)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -710,8 +710,28 @@ def wl_topk(args) -> dict:
     return rec
 
 
+def wl_c3_launches(args) -> dict:
+    """Counter driver: `--steps` eager launches of the C3 prefill alone (no
+    graph, no other kernels), for rocprofv3 --pmc passes over exactly the
+    prefill dispatches."""
+    import torch
+
+    from vllm_apple_amd import kernels, workloads
+
+    b = workloads.c3_prefill(device=torch.device("cuda:0"))
+    out = torch.empty_like(b.query)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        kernels.paged_prefill(b.query, b.k_cache, b.v_cache, b.block_table, b.token_to_seq,
+                              b.positions, scale=b.scale, output=out)
+    torch.cuda.synchronize()
+    return {"workload": "C3-launches", "launches": args.steps,
+            "note": "eager C3 prefill launches for counter collection"}
+
+
 WORKLOADS = {"C1": wl_c1, "C2u": wl_c2u, "C3": wl_c3, "C4": wl_c4, "C5": wl_c5,
-             "C5mlp": wl_c5mlp, "C2bf16": wl_c2bf16, "topk": wl_topk}
+             "C5mlp": wl_c5mlp, "C2bf16": wl_c2bf16, "topk": wl_topk,
+             "C3-launches": wl_c3_launches}
 
 
 def main() -> int:
