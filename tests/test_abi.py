@@ -242,6 +242,16 @@ def test_balanced_shared_workspace(lib):
     assert two > one > 0
     p.partition_size = -3
     assert lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part)) == 0
+    # Fixed partitions index the grid's y dimension: at most 65535 of them.
+    p.partition_size = 128
+    p.max_blocks_per_seq = 1 << 20
+    p.max_seq_len = 128 * 65535
+    assert lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part)) > 0
+    p.max_seq_len = 128 * 65535 + 1
+    assert lib.vaa_paged_attention_decode_workspace_size(ctypes.byref(p), ctypes.byref(part)) == 0
+    st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
+                                        None, None, None, 0, None)
+    assert st != 0
 
 
 def test_wide_groups_and_merge_arguments(lib):

@@ -417,15 +417,19 @@ __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int seq) {
   return L > cap ? cap : L;
 }
 
-// Fixed partitions: grid (partition, kv_head, seq).  NW waves per workgroup:
-// 8 for long partitions; 4 for short ones, so that two workgroups share a CU
-// and one's start-up (Q load, first tiles) overlaps the other's tail.
+// Fixed partitions: grid (kv_head x head chunk, partition, seq), the kv head
+// fastest: consecutive workgroups read the same cache blocks' heads, which lie
+// side by side in HBM ([block][kv head][token][dim]), at about the same time
+// (C4 with 512-token partitions: 62 -> 68 % of HBM peak against partition
+// fastest).  NW waves per workgroup: 8 for long partitions; 4 for short
+// ones, so that two workgroups share a CU and one's start-up (Q load, first
+// tiles) overlaps the other's tail.
 template <int D, typename T, int NW>
 __global__ void __launch_bounds__(NW* kWave)
 paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int part = blockIdx.x, seq = blockIdx.z;
-  const int kvh = blockIdx.y / a.chunks, hc = blockIdx.y % a.chunks;
+  const int part = blockIdx.y, seq = blockIdx.z;
+  const int kvh = blockIdx.x / a.chunks, hc = blockIdx.x % a.chunks;
   const int qh0 = kvh * a.G + hc * a.Gc, nh = min(a.Gc, a.G - hc * a.Gc);
   const int Lorig = a.seq_lens[seq];
   const int L = clamped_len(a, seq);
@@ -748,6 +752,11 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
                 (long long)part, VAA_PARTITION_BALANCED, VAA_PARTITION_BALANCED_SHARED);
   }
   if (part > (int64_t{1} << 30)) part = int64_t{1} << 30;
+  // Partitions index the grid's y dimension.
+  if ((max_len + part - 1) / part > 65535)
+    return fail(VAA_ERR_UNSUPPORTED,
+                "partition_size=%lld splits max_seq_len=%lld into more than 65535 partitions",
+                (long long)part, (long long)max_len);
   sp->balanced = false;
   sp->shared = false;
   sp->part = static_cast<int>(part);
@@ -824,7 +833,7 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
                        dim3(D), 0, stream, a);
     return check_launch("paged_decode_merge_balanced_kernel");
   }
-  dim3 grid(a.max_parts, a.num_kv_heads * a.chunks, a.num_seqs);
+  dim3 grid(a.num_kv_heads * a.chunks, a.max_parts, a.num_seqs);
   if (a.max_parts > 1 && a.part_tiles <= kShortPartTiles) {
     constexpr int kNw = kWaves / 2;
     const size_t lds4 = std::max(static_cast<size_t>(kNw) * kTile * D * sizeof(f16),
