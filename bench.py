@@ -472,10 +472,16 @@ def wl_c5(args) -> dict:
                              b.seq_lens[:nd], scale=b.scale, max_seq_len=max(lens[:nd]),
                              output=out[:nd], seq_lens_host=lens[:nd], shared=shared)
 
-    def prefill():
+    # The key split the backend chooses for these prefill chunks when they run
+    # alone; next to the decode it runs them unsplit.
+    qlens = [0] * nd + [256] * (b.num_seqs - nd)
+    split = kernels.choose_prefill_split(lens, qlens, b.num_kv_heads, b.num_q_heads,
+                                         kernels.device_cus(dev))
+
+    def prefill(split_keys=0):
         kernels.paged_prefill(b.query[nd:], b.k_cache, b.v_cache, b.block_table,
                               b.token_to_seq[nd:], b.positions[nd:], scale=b.scale,
-                              output=out[nd:])
+                              output=out[nd:], split_keys=split_keys, max_seq_len=max(lens))
 
     def attn_step():
         # As the backend runs a mixed step: the KV write, then prefill (current
@@ -486,10 +492,13 @@ def wl_c5(args) -> dict:
     def attn_step_serial():
         kernels.kv_write_slots(b.new_k, b.new_v, b.k_cache, b.v_cache, b.slot_mapping)
         decode()
-        prefill()
+        prefill(split)
 
     t_attn = _timed(attn_step, args.steps, args.warmup)
     t_attn_serial = _timed(attn_step_serial, args.steps, args.warmup)
+    t_prefill = _timed(lambda: prefill(split), args.steps, args.warmup)
+    t_prefill_whole = _timed(prefill, args.steps, args.warmup)
+    t_decode = _timed(decode, args.steps, args.warmup)
     # Eager calls too: vLLM runs the attention of mixed batches outside graphs.
     t_attn_eager = _timed_eager(attn_step, args.steps)
     t_attn_serial_eager = _timed_eager(attn_step_serial, args.steps)
@@ -574,6 +583,9 @@ def wl_c5(args) -> dict:
            "attention_step_serial_ms": round(t_attn_serial, 5),
            "attention_step_eager_ms": round(t_attn_eager, 5),
            "attention_step_serial_eager_ms": round(t_attn_serial_eager, 5),
+           "prefill_split_keys": split,
+           "prefill_ms": round(t_prefill, 5), "prefill_unsplit_ms": round(t_prefill_whole, 5),
+           "decode_ms": round(t_decode, 5),
            "attention_decode_kv_bytes": kv_read,
            "attention_prefill_flops": 4.0 * D * H * pre_ctx}
     rec["qkv_epilogue_three_pass_ms"] = round(t_three, 5)

@@ -275,6 +275,28 @@ int vaa_paged_attention_prefill(const vaa_attn_params* p, const uint16_t* query,
                                 int num_tokens, void* stream);
 
 /*
+ * The same prefill with split-K over the keys, for batches whose contexts
+ * are unequal (a long prefix next to short ones): key tiles are cut into
+ * pieces of split_keys positions (a positive multiple of 64; the last piece
+ * takes any excess past p->max_seq_len), one workgroup per (query tile, kv
+ * head, piece), and rows whose context spans several pieces are combined by
+ * a log-sum-exp merge -- the split/merge structure of
+ * paged_attention_v2.metal's partitions (:49-261) applied to the prefill
+ * kernel (:375-478).  Same results and unwritten-row rules as
+ * vaa_paged_attention_prefill.  workspace: at least
+ * vaa_paged_attention_prefill_workspace_size(p, num_tokens, split_keys) bytes,
+ * 16-byte aligned (0 bytes when max_seq_len fits one piece).
+ */
+size_t vaa_paged_attention_prefill_workspace_size(const vaa_attn_params* p, int num_tokens,
+                                                  int split_keys);
+int vaa_paged_attention_prefill_split(const vaa_attn_params* p, const uint16_t* query,
+                                      const uint16_t* key_cache, const uint16_t* value_cache,
+                                      const int32_t* block_table, const int32_t* token_to_seq,
+                                      const int32_t* positions, uint16_t* output,
+                                      int num_tokens, int split_keys, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+
+/*
  * token_to_seq and positions for a flattened batch, computed on the device
  * from query_start_loc [num_seqs+1] and full seq_lens [num_seqs]:
  *   token_to_seq = repeat_interleave(arange(num_seqs), diff(query_start_loc))

@@ -254,6 +254,33 @@ def test_balanced_shared_workspace(lib):
     assert st != 0
 
 
+def test_prefill_split_arguments(lib):
+    """The split prefill sizes its partials from max_seq_len, needs no
+    workspace when max_seq_len fits one piece, and refuses split sizes that
+    are not positive multiples of 64 before any launch."""
+    from vllm_apple_amd import _lib
+
+    p = _lib.VaaAttnParams()
+    p.head_size, p.block_size, p.num_kv_heads, p.num_query_heads = 128, 16, 8, 32
+    p.queries_per_kv, p.num_seqs, p.max_blocks_per_seq, p.num_blocks = 4, 8, 1024, 8192
+    p.max_seq_len = 16384
+    size = lib.vaa_paged_attention_prefill_workspace_size
+    assert size(ctypes.byref(p), 2048, 4096) == 2048 * 32 * 4 * (128 + 2) * 4
+    assert size(ctypes.byref(p), 2048, 16384) == 0  # one piece
+    assert size(ctypes.byref(p), 2048, 100) == 0 and "multiple of 64" in _lib.last_error()
+    st = lib.vaa_paged_attention_prefill_split(ctypes.byref(p), None, None, None, None, None,
+                                               None, None, 16, 96, None, 0, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "split_keys=96" in _lib.last_error()
+    st = lib.vaa_paged_attention_prefill_split(ctypes.byref(p), None, None, None, None, None,
+                                               None, None, 16, 0, None, 0, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG
+    p.max_blocks_per_seq = 1 << 20
+    p.max_seq_len = 64 * 1025  # more than 1024 pieces of 64 keys
+    st = lib.vaa_paged_attention_prefill_split(ctypes.byref(p), None, None, None, None, None,
+                                               None, None, 16, 64, None, 0, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED
+
+
 def test_wide_groups_and_merge_arguments(lib):
     """GQA groups above 16 heads have a workspace size (head chunks), the
     state merge checks its arguments, and the single-token KV write rejects an

@@ -425,3 +425,42 @@ def test_forward_mixed_overlap_balanced_shared_split(gpu, monkeypatch):
     assert_close(outs["1"], ref, what="overlapped mixed step (shared split)")
     assert_close(outs["0"], ref, what="serial mixed step")
     assert np.array_equal(outs["0"][len(dec):], outs["1"][len(dec):]), "prefill rows"
+
+
+@pytest.mark.parametrize("dec_lens", [(), (37, 300)])
+def test_forward_prefill_split_with_host_lengths(gpu, monkeypatch, dec_lens):
+    """With the host lengths in the metadata, a prefill-only batch with one
+    long context next to short ones runs the split-K prefill (the chooser's
+    split); beside decodes (run concurrently) the prefill stays unsplit.
+    Every row matches the oracle either way."""
+    from vllm_apple_amd import kernels
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    print(f"[case] backend prefill split, decodes {dec_lens}", flush=True)
+    b = _mixed_batch(seed=7, dec_lens=dec_lens, pre=((12000, 256), (300, 256), (700, 256)))
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    scale = 1 / math.sqrt(D)
+    impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv = b["qkv"].to(dev)
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    kv_cache = b["kv_cache"].to(dev)
+    md = _metadata(b, dev)
+    md._seq_lens_cpu = b["lens"].tolist()
+    md._query_start_loc_cpu = b["qsl"].tolist()
+    seen = []
+    real = kernels.paged_prefill
+
+    def spy(*args, **kw):
+        seen.append(kw.get("split_keys", 0))
+        return real(*args, **kw)
+
+    monkeypatch.setattr(kernels, "paged_prefill", spy)
+    out = torch.zeros((T, H, D), dtype=torch.float16, device=dev)
+    impl.forward(None, q, k, v, kv_cache, md, output=out)
+    torch.cuda.synchronize()
+    assert seen and (seen[0] > 0) == (len(dec_lens) == 0)
+    ref, kc, vc = _oracle(b, scale)
+    assert_close(host(out), ref, what="forward with split prefill")

@@ -227,3 +227,21 @@ def test_partition_choice_small_batches():
     assert K.choose_partition_size([162, 125, 444, 341], 2, 256) >= 444  # C1: unsplit
     assert K.choose_partition_size([8192] * 32, 8, 256) == 8192          # headline: unsplit
     assert K.choose_partition_size(list(range(1024, 8192, 224)), 8, 256) == K.PARTITION_BALANCED
+
+
+def test_prefill_split_choice():
+    """Key splits only for unequal contexts: C3 (four equal 2560-token
+    contexts) stays whole; C5's prefill chunks (256 tokens over contexts up to
+    16k, one of them far longer than the per-slot share) are split into pieces
+    of a multiple of 1024 keys, shorter than the longest context."""
+    from vllm_apple_amd import kernels as K
+
+    K._prefill_split_cache.clear()
+    assert K.choose_prefill_split([2560] * 4, [512] * 4, 8, 32, 256) == 0
+    c5 = [16000, 600, 900, 2000, 3000, 1200, 800, 700]
+    sp = K.choose_prefill_split(c5, [256] * 8, 8, 32, 256)
+    assert sp > 0 and sp % 1024 == 0 and sp < 16000
+    # decodes (query length 0 here) and empty sequences carry no prefill work
+    assert K.choose_prefill_split([16000, 500], [0, 0], 8, 32, 256) == 0
+    # short contexts never split
+    assert K.choose_prefill_split([2000, 100], [64, 64], 8, 32, 256) == 0

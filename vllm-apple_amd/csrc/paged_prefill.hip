@@ -44,6 +44,7 @@ constexpr int kWavesP = 4;    // waves per workgroup
 constexpr int kXcds = 8;      // accelerator complex dies on MI355X
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
 constexpr int kThreadsP = kWavesP * kWave;
+constexpr int kMaxPrefillSplits = 1024;  // grid z of the split-K prefill
 static_assert(kKT == 16 * kWavesP, "one 16-key group per wave");
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -63,6 +64,15 @@ struct PrefillArgs {
   int bs_shift;               // log2(block_size) when it is a power of two, else -1
   int heads_per_wg, subtiles, head_chunks;
   int tiles_y, padded_tiles;  // logical grid rows; workgroups in use (multiple of 8)
+  // Split-K over the keys (grid z): split z covers key tiles
+  // [z*split_tiles, (z+1)*split_tiles), the last one the rest.  A row whose
+  // context spans more than one split leaves a partial (unnormalised O, max
+  // in the log2 domain, sum) per split in row (token*H + head)*n_splits + z
+  // of ws_acc / ws_ml, and prefill_merge_kernel writes its output; split 0
+  // writes the other rows directly.  split_tiles = 0: no split.
+  int split_tiles, n_splits, num_q_heads;
+  float* ws_acc;
+  float* ws_ml;
   int64_t num_blocks;
   int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
   int64_t q_st, q_sh, o_st, o_sh;
@@ -212,6 +222,13 @@ __device__ __forceinline__ int first_bad_key(const PrefillArgs& a, const int32_t
   }
   bad = wave_min_i(bad);
   return bad == INT32_MAX ? INT32_MAX : bad * a.block_size;
+}
+
+// Splits a row at position pos spans: its context [0, pos] covers
+// ceil((pos + 1) / kKT) key tiles; the last split takes any excess.
+__device__ __forceinline__ int row_splits(const PrefillArgs& a, int pos) {
+  const int tiles = (pos + kKT) / kKT;
+  return min(a.n_splits, (tiles + a.split_tiles - 1) / a.split_tiles);
 }
 
 // Streams one 64-key tile into (kd, vd): wave w copies 16-key group w with
@@ -407,6 +424,7 @@ paged_prefill_kernel(PrefillArgs a) {
   const int logical = (id % kXcds) * per_xcd + kx;
   if (logical >= gx * a.tiles_y) return;
   const int tile_x = logical % gx, tile_y = logical / gx;
+  const int split = blockIdx.z;
   const int kvh = tile_y / a.head_chunks;
   const int hchunk = tile_y % a.head_chunks;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -474,35 +492,72 @@ paged_prefill_kernel(PrefillArgs a) {
     const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
     const int lim = active ? tpos : -1;  // last key position this row may see
     if (lim >= first_bad_key(a, bts, kv_len, lane)) aborted = true;
+    // This workgroup's key tiles of the sequence: all of them, or its split.
+    int t_lo = 0, t_hi = n_kt;
+    if (a.split_tiles > 0) {
+      t_lo = split * a.split_tiles;
+      if (split != a.n_splits - 1) t_hi = min(n_kt, t_lo + a.split_tiles);
+    }
 
     // Double buffer: the next tile's direct loads are issued before this
     // tile's math; one wait + barrier per tile publishes it.
-    BlockWindow win;
-    window_load(a, bts, 0, win);
-    tile_fetch<D>(a, bts, kbase, vbase, 0, kv_len, wave, lane, L, win, k0s, v0s);
-    wait_all();
-    __builtin_amdgcn_s_barrier();
-    for (int kt = 0; kt < n_kt; kt += 2) {
-      if (kt + 1 < n_kt)
-        tile_fetch<D>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
-                      v1s);
-      if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
+    if (t_lo < t_hi) {
+      BlockWindow win;
+      window_load(a, bts, a.bs_shift >= 0 ? (t_lo * kKT) >> a.bs_shift
+                                          : (t_lo * kKT) / a.block_size, win);
+      tile_fetch<D>(a, bts, kbase, vbase, t_lo * kKT, kv_len, wave, lane, L, win, k0s, v0s);
       wait_all();
       __builtin_amdgcn_s_barrier();
-      if (kt + 1 >= n_kt) break;
-      if (kt + 2 < n_kt)
-        tile_fetch<D>(a, bts, kbase, vbase, (kt + 2) * kKT, kv_len, wave, lane, L, win, k0s,
-                      v0s);
-      if (math) tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
-      wait_all();
-      __builtin_amdgcn_s_barrier();
+      for (int kt = t_lo; kt < t_hi; kt += 2) {
+        if (kt + 1 < t_hi)
+          tile_fetch<D>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
+                        v1s);
+        if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
+        wait_all();
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 >= t_hi) break;
+        if (kt + 2 < t_hi)
+          tile_fetch<D>(a, bts, kbase, vbase, (kt + 2) * kKT, kv_len, wave, lane, L, win, k0s,
+                        v0s);
+        if (math)
+          tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
+        wait_all();
+        __builtin_amdgcn_s_barrier();
+      }
     }
     done = done || active;
   }
 
   if (!math) return;
   const float l_tot = half_sum(l_part);
-  if (!row_ok || aborted) return;
+  if (!row_ok) return;
+  if (a.split_tiles > 0) {
+    const int rs = row_splits(a, tpos);
+    if (rs > 1) {
+      // Partial of this split (fully masked: max -inf, sum 0); an aborted
+      // row is marked by a negative sum, which the merge leaves unwritten.
+      if (split >= rs) return;
+      const int64_t row =
+          (static_cast<int64_t>(tok) * a.num_q_heads + head) * a.n_splits + split;
+      float* dst = a.ws_acc + row * D;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) {
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const f32x4 v = {acc[dt][4 * rg], acc[dt][4 * rg + 1], acc[dt][4 * rg + 2],
+                           acc[dt][4 * rg + 3]};
+          *reinterpret_cast<f32x4*>(dst + 32 * dt + 8 * rg + 4 * hb) = v;
+        }
+      }
+      if (hb == 0) {
+        a.ws_ml[row * 2 + 0] = m_run;
+        a.ws_ml[row * 2 + 1] = aborted ? -1.f : l_tot;
+      }
+      return;
+    }
+    if (split != 0) return;  // the row's keys all lie in split 0
+  }
+  if (aborted) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   f16* op = a.out + static_cast<int64_t>(tok) * a.o_st + head * a.o_sh;
 #pragma unroll
@@ -518,6 +573,35 @@ paged_prefill_kernel(PrefillArgs a) {
   }
 }
 
+// Log-sum-exp merge of a split row's partials (one workgroup per (token,
+// head), a thread per dimension): out = sum_z 2^(m_z - M) acc_z / sum_z
+// 2^(m_z - M) l_z.  Rows the reference leaves unwritten stay untouched: the
+// same validity rules as the attention kernel, and the abort mark of split 0.
+template <int D, typename T>
+__global__ void __launch_bounds__(D) prefill_merge_kernel(PrefillArgs a) {
+  const int tok = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+  const int seq = a.tok_seq[tok], pos = a.pos[tok];
+  if (seq < 0 || seq >= a.num_seqs || pos < 0) return;
+  if ((static_cast<int64_t>(pos) + a.block_size) / a.block_size > a.max_blocks) return;
+  const int rs = row_splits(a, pos);
+  if (rs <= 1) return;
+  const int64_t row0 = (static_cast<int64_t>(tok) * a.num_q_heads + head) * a.n_splits;
+  if (a.ws_ml[row0 * 2 + 1] < 0.f) return;  // aborted
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int z = 0; z < rs; ++z) {
+    const float mz = a.ws_ml[(row0 + z) * 2], lz = a.ws_ml[(row0 + z) * 2 + 1];
+    if (!(lz > 0.f)) continue;
+    const float az = a.ws_acc[(row0 + z) * D + d];
+    const float Mn = fmaxf(M, mz);
+    const float so = fast_exp2(M - Mn), sn = fast_exp2(mz - Mn);
+    num = num * so + az * sn;
+    den = den * so + lz * sn;
+    M = Mn;
+  }
+  reinterpret_cast<T*>(a.out)[static_cast<int64_t>(tok) * a.o_st + head * a.o_sh + d] =
+      Elem<T>::from_f(den > 0.f ? num / den : 0.f);
+}
+
 template <int D, typename T>
 int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   const int per_wg = kQT * a.subtiles;
@@ -528,9 +612,13 @@ int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   PrefillArgs b = a;
   b.tiles_y = gy;
   b.padded_tiles = padded;
-  dim3 grid(gx, (padded + gx - 1) / gx);
+  dim3 grid(gx, (padded + gx - 1) / gx, a.split_tiles > 0 ? a.n_splits : 1);
   hipLaunchKernelGGL((paged_prefill_kernel<D, T>), grid, dim3(kThreadsP), 0, stream, b);
-  return check_launch("paged_prefill_kernel");
+  const int st = check_launch("paged_prefill_kernel");
+  if (st || a.split_tiles <= 0) return st;
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(a.num_tokens, a.num_q_heads), dim3(D), 0,
+                     stream, b);
+  return check_launch("prefill_merge_kernel");
 }
 
 }  // namespace
@@ -538,50 +626,95 @@ int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
 
 using namespace vaa;
 
-extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
-                                           const uint16_t* query,
-                                           const uint16_t* key_cache,
-                                           const uint16_t* value_cache,
-                                           const int32_t* block_table,
-                                           const int32_t* token_to_seq,
-                                           const int32_t* positions,
-                                           uint16_t* output, int num_tokens,
-                                           void* stream) {
-  if (!p) return fail(VAA_ERR_INVALID_ARG, "vaa_paged_attention_prefill: null params");
+namespace vaa {
+namespace {
+
+// Split-K plan for max_seq_len: key tiles per split and the number of splits.
+int prefill_split_plan(const char* what, const vaa_attn_params* p, int split_keys,
+                       int* split_tiles, int* n_splits) {
+  if (split_keys <= 0 || split_keys % kKT != 0)
+    return fail(VAA_ERR_INVALID_ARG, "%s: split_keys=%d must be a positive multiple of %d",
+                what, split_keys, kKT);
+  int64_t max_len = p->max_seq_len;
+  const int64_t cap = static_cast<int64_t>(p->max_blocks_per_seq) * p->block_size;
+  if (max_len > cap) max_len = cap;
+  if (max_len < 1) max_len = 1;
+  const int64_t tiles = (max_len + kKT - 1) / kKT, per = split_keys / kKT;
+  const int64_t ns = (tiles + per - 1) / per;
+  if (ns > kMaxPrefillSplits)
+    return fail(VAA_ERR_UNSUPPORTED, "%s: split_keys=%d cuts max_seq_len=%lld into %lld > %d splits",
+                what, split_keys, (long long)max_len, (long long)ns, kMaxPrefillSplits);
+  *split_tiles = static_cast<int>(per);
+  *n_splits = static_cast<int>(ns);
+  return VAA_OK;
+}
+
+size_t prefill_ws_bytes(const vaa_attn_params* p, int num_tokens, int n_splits) {
+  if (n_splits <= 1 || num_tokens <= 0) return 0;
+  return static_cast<size_t>(num_tokens) * p->num_query_heads * n_splits *
+         (static_cast<size_t>(p->head_size) + 2) * sizeof(float);
+}
+
+int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* query,
+                 const uint16_t* key_cache, const uint16_t* value_cache,
+                 const int32_t* block_table, const int32_t* token_to_seq,
+                 const int32_t* positions, uint16_t* output, int num_tokens, int split_keys,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  if (!p) return fail(VAA_ERR_INVALID_ARG, "%s: null params", what);
   if (p->head_size != 32 && p->head_size != 64 && p->head_size != 96 &&
       p->head_size != 128)
-    return fail(VAA_ERR_UNSUPPORTED,
-                "vaa_paged_attention_prefill: head_size=%d not in {32,64,96,128}",
+    return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d not in {32,64,96,128}", what,
                 p->head_size);
   if (p->block_size <= 0 || p->num_kv_heads <= 0 || p->num_query_heads <= 0 ||
       p->num_query_heads % p->num_kv_heads != 0 ||
       p->queries_per_kv != p->num_query_heads / p->num_kv_heads ||
       p->max_blocks_per_seq <= 0 || p->num_blocks <= 0 || p->num_seqs < 0 ||
       num_tokens < 0)
-    return fail(VAA_ERR_INVALID_ARG, "vaa_paged_attention_prefill: bad shape params");
+    return fail(VAA_ERR_INVALID_ARG, "%s: bad shape params", what);
   if (p->block_size % 16 != 0)
-    return fail(VAA_ERR_UNSUPPORTED,
-                "vaa_paged_attention_prefill: block_size=%d is not a multiple of 16",
+    return fail(VAA_ERR_UNSUPPORTED, "%s: block_size=%d is not a multiple of 16", what,
                 p->block_size);
   if (!valid_dtype(p->dtype))
-    return fail(VAA_ERR_UNSUPPORTED, "vaa_paged_attention_prefill: dtype=%d", p->dtype);
+    return fail(VAA_ERR_UNSUPPORTED, "%s: dtype=%d", what, p->dtype);
+  if (p->num_query_heads > 65535)
+    return fail(VAA_ERR_UNSUPPORTED, "%s: num_query_heads=%d", what, p->num_query_heads);
+  int split_tiles = 0, n_splits = 1;
+  if (split_keys != 0) {
+    const int st = prefill_split_plan(what, p, split_keys, &split_tiles, &n_splits);
+    if (st) return st;
+    if (n_splits <= 1) split_tiles = 0;  // one split: the plain kernel
+  }
   if (num_tokens == 0) return VAA_OK;
   if (!query || !key_cache || !value_cache || !block_table || !token_to_seq ||
       !positions || !output)
-    return fail(VAA_ERR_INVALID_ARG, "vaa_paged_attention_prefill: null pointer");
+    return fail(VAA_ERR_INVALID_ARG, "%s: null pointer", what);
   const int64_t strides[] = {p->k_stride_block, p->k_stride_head, p->k_stride_token,
                              p->v_stride_block, p->v_stride_head, p->v_stride_token,
                              p->q_stride_token, p->q_stride_head, p->o_stride_token,
                              p->o_stride_head};
   for (int64_t s : strides)
     if (s < 0 || s % 8 != 0)
-      return fail(VAA_ERR_INVALID_ARG,
-                  "vaa_paged_attention_prefill: strides must be multiples of 8 elements");
+      return fail(VAA_ERR_INVALID_ARG, "%s: strides must be multiples of 8 elements", what);
   if (!aligned16(query) || !aligned16(key_cache) || !aligned16(value_cache) ||
       !aligned16(output))
-    return fail(VAA_ERR_INVALID_ARG,
-                "vaa_paged_attention_prefill: tensors must be 16-byte aligned");
+    return fail(VAA_ERR_INVALID_ARG, "%s: tensors must be 16-byte aligned", what);
   PrefillArgs a;
+  a.split_tiles = split_tiles;
+  a.n_splits = n_splits;
+  a.num_q_heads = p->num_query_heads;
+  a.ws_acc = nullptr;
+  a.ws_ml = nullptr;
+  if (split_tiles > 0) {
+    const size_t need = prefill_ws_bytes(p, num_tokens, n_splits);
+    if (!workspace || workspace_bytes < need)
+      return fail(VAA_ERR_WORKSPACE, "%s: workspace %zu bytes < %zu needed", what,
+                  workspace_bytes, need);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+      return fail(VAA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", what);
+    const size_t rows = static_cast<size_t>(num_tokens) * p->num_query_heads * n_splits;
+    a.ws_acc = static_cast<float*>(workspace);
+    a.ws_ml = a.ws_acc + rows * p->head_size;
+  }
   a.q = reinterpret_cast<const f16*>(query);
   a.kc = reinterpret_cast<const f16*>(key_cache);
   a.vc = reinterpret_cast<const f16*>(value_cache);
@@ -626,4 +759,51 @@ extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
                         : launch_prefill<128, f16>(a, p->num_kv_heads, s);
   }
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
+}
+
+}  // namespace
+}  // namespace vaa
+
+extern "C" int vaa_paged_attention_prefill(const vaa_attn_params* p,
+                                           const uint16_t* query,
+                                           const uint16_t* key_cache,
+                                           const uint16_t* value_cache,
+                                           const int32_t* block_table,
+                                           const int32_t* token_to_seq,
+                                           const int32_t* positions,
+                                           uint16_t* output, int num_tokens,
+                                           void* stream) {
+  return prefill_impl("vaa_paged_attention_prefill", p, query, key_cache, value_cache,
+                      block_table, token_to_seq, positions, output, num_tokens, 0, nullptr, 0,
+                      stream);
+}
+
+extern "C" size_t vaa_paged_attention_prefill_workspace_size(const vaa_attn_params* p,
+                                                             int num_tokens, int split_keys) {
+  if (!p || p->max_blocks_per_seq <= 0 || p->block_size <= 0 || p->num_query_heads <= 0)
+    return 0;
+  int split_tiles = 0, n_splits = 1;
+  if (prefill_split_plan("vaa_paged_attention_prefill_workspace_size", p, split_keys,
+                         &split_tiles, &n_splits) != VAA_OK)
+    return 0;
+  return prefill_ws_bytes(p, num_tokens, n_splits);
+}
+
+extern "C" int vaa_paged_attention_prefill_split(const vaa_attn_params* p,
+                                                 const uint16_t* query,
+                                                 const uint16_t* key_cache,
+                                                 const uint16_t* value_cache,
+                                                 const int32_t* block_table,
+                                                 const int32_t* token_to_seq,
+                                                 const int32_t* positions, uint16_t* output,
+                                                 int num_tokens, int split_keys,
+                                                 void* workspace, size_t workspace_bytes,
+                                                 void* stream) {
+  if (split_keys == 0)
+    return fail(VAA_ERR_INVALID_ARG,
+                "vaa_paged_attention_prefill_split: split_keys must be a positive multiple of %d",
+                kKT);
+  return prefill_impl("vaa_paged_attention_prefill_split", p, query, key_cache, value_cache,
+                      block_table, token_to_seq, positions, output, num_tokens, split_keys,
+                      workspace, workspace_bytes, stream);
 }

@@ -94,6 +94,9 @@ SIGNATURES = {
     "vaa_paged_attention_decode_workspace_size": (ctypes.c_size_t, [_PARAMS, ctypes.POINTER(ctypes.c_int32)]),
     "vaa_paged_attention_decode": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "vaa_paged_attention_prefill": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "vaa_paged_attention_prefill_workspace_size": (ctypes.c_size_t, [_PARAMS, _I, _I]),
+    "vaa_paged_attention_prefill_split": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P,
+                                               ctypes.c_size_t, _P]),
     "vaa_paged_attention_decode_noalloc_max_workspace": (ctypes.c_size_t, []),
     "vaa_paged_attention_decode_noalloc": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "vaa_merge_attn_states": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _I64, _I64, _P, _I, _P]),

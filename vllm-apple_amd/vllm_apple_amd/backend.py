@@ -301,15 +301,32 @@ class HipAttentionImpl(AttentionImpl):
                                      seq_lens_host=lens_host[:nd] if lens_host else None,
                                      shared=shared)
 
+            overlapped = nd > 0 and n > nd and _overlap_enabled()
+
             def prefill():
+                # Split long contexts when the host lengths are at hand (never
+                # a device sync for them) and no decode runs beside the
+                # prefill: next to a decode the unsplit prefill is better (its
+                # long workgroups hold a few CUs and leave the rest to the
+                # decode; C5 attention step 0.61 ms against 0.68-0.79 split).
+                split = 0
+                lens_host = attn_metadata._seq_lens_cpu
+                qsl_host = attn_metadata._query_start_loc_cpu
+                if lens_host and qsl_host and not overlapped:
+                    pl = [b - a for a, b in zip(qsl_host[:-1], qsl_host[1:])]
+                    split = kernels.choose_prefill_split(
+                        lens_host, [q if q > 1 else 0 for q in pl], self.num_kv_heads,
+                        query.shape[1], kernels.device_cus(query.device))
                 kernels.paged_prefill(query[nd:n], key_cache, value_cache,
                                       attn_metadata.block_table, tok[nd:n], pos[nd:n],
-                                      scale=self.scale, layout="vllm", output=output[nd:n])
+                                      scale=self.scale, layout="vllm", output=output[nd:n],
+                                      split_keys=split,
+                                      max_seq_len=attn_metadata.max_seq_len if split else 0)
 
             if n > nd:
                 tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,
                                                      attn_metadata.seq_lens, n)
-            if nd > 0 and n > nd and _overlap_enabled():
+            if overlapped:
                 # Mixed step: prefill (MFMA-bound, current stream, dispatched
                 # first) and decode (HBM-bound, side stream, shared split) run
                 # concurrently.

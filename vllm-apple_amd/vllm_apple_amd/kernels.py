@@ -486,16 +486,77 @@ def merge_attn_states(partial_out: torch.Tensor, partial_lse: torch.Tensor, *,
     return output
 
 
+_prefill_ws = _GrowOnlyScratch()
+_PREFILL_KEY_TILE = 64      # keys per prefill tile (paged_prefill.hip)
+_PREFILL_SPLIT_QUANTUM = 1024  # split sizes in multiples of 16 key tiles
+_prefill_split_cache: dict = {}
+
+
+def choose_prefill_split(ctx_lens_host, query_lens_host, num_kv_heads: int,
+                         num_query_heads: int, num_cus: int) -> int:
+    """Key split for a prefill batch (0: none), from the host lengths.
+
+    The prefill kernel gives each workgroup a query tile (32 tokens of 4
+    heads, or the same rows over fewer heads) and streams that sequence's
+    whole context, so one long context next to short ones makes the longest
+    workgroups the critical path while the others leave CUs idle.  Work is
+    counted in 64-key tiles per workgroup; with two workgroups per CU the
+    per-slot share is total / (2 * CUs).  A split is chosen when the longest
+    workgroup exceeds 1.5x that share, with pieces of about half the share
+    (rounded up to 1024 keys) so the dispatcher can balance the pieces.
+    Memoised per length tuple (every layer of a step sees the same batch).
+    """
+    key = (tuple(int(x) for x in ctx_lens_host), tuple(int(x) for x in query_lens_host),
+           int(num_kv_heads), int(num_query_heads), int(num_cus))
+    hit = _prefill_split_cache.get(key)
+    if hit is not None:
+        return hit
+    g = max(1, num_query_heads // max(1, num_kv_heads))
+    heads_per_wg = 4 if g >= 4 else (3 if g == 3 else g)
+    tokens_per_wg = 32 * (1 if g >= 3 else 4 // g)
+    chunks = -(-g // heads_per_wg)
+    total, longest = 0, 0
+    for ctx, q in zip(key[0], key[1]):
+        if q <= 0 or ctx <= 0:
+            continue
+        tiles = -(-ctx // _PREFILL_KEY_TILE)
+        total += -(-q // tokens_per_wg) * tiles
+        longest = max(longest, tiles)
+    total *= num_kv_heads * chunks
+    share = total / max(1, 2 * num_cus)
+    split = 0
+    if longest > 32 and longest > 1.5 * share:
+        piece = max(_PREFILL_SPLIT_QUANTUM, int(share / 2) * _PREFILL_KEY_TILE)
+        split = -(-piece // _PREFILL_SPLIT_QUANTUM) * _PREFILL_SPLIT_QUANTUM
+        if split >= longest * _PREFILL_KEY_TILE:
+            split = 0
+    if len(_prefill_split_cache) > 4096:
+        _prefill_split_cache.clear()
+    _prefill_split_cache[key] = split
+    return split
+
+
+def prefill_workspace_size(p: _lib.VaaAttnParams, num_tokens: int, split_keys: int) -> int:
+    return int(_lib.load().vaa_paged_attention_prefill_workspace_size(
+        ctypes.byref(p), int(num_tokens), int(split_keys)))
+
+
 def paged_prefill(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                   block_table: torch.Tensor, token_to_seq: torch.Tensor,
                   positions: torch.Tensor, *, scale: float, layout: str = "kernel",
-                  output: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+                  output: torch.Tensor | None = None, split_keys: int = 0,
+                  max_seq_len: int = 0, workspace: torch.Tensor | None = None,
+                  stream=None) -> torch.Tensor:
     """Chunked-prefill attention: token t attends to cache positions [0, positions[t]].
 
     query [num_tokens, H, D] fp16 or bf16, as the caches and output; the
     tokens' own K/V must already be cached.
     Rows the reference kernel leaves unwritten (invalid sequence, negative
     position, context past the block table, invalid block) stay untouched.
+    split_keys > 0 cuts each context into pieces of that many keys (a
+    multiple of 64; see choose_prefill_split) merged by log-sum-exp;
+    max_seq_len bounds the contexts (default: the block table's capacity) and
+    sizes the partials' workspace (grow-only scratch unless given).
     """
     _require_gpu(query, key_cache, value_cache, block_table, token_to_seq, positions, output)
     dt = _attn_dtype(query=query, key_cache=key_cache, value_cache=value_cache, output=output)
@@ -512,10 +573,25 @@ def paged_prefill(query: torch.Tensor, key_cache: torch.Tensor, value_cache: tor
     p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
                     num_query_heads=query.shape[1], scale=scale, num_seqs=block_table.shape[0],
                     max_blocks_per_seq=block_table.shape[1], query=query, output=output)
-    _lib.call("vaa_paged_attention_prefill", ctypes.byref(p), query.data_ptr(),
+    if not split_keys:
+        _lib.call("vaa_paged_attention_prefill", ctypes.byref(p), query.data_ptr(),
+                  key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
+                  token_to_seq.data_ptr(), positions.data_ptr(), output.data_ptr(), num_tokens,
+                  _lib.stream_handle(stream))
+        return output
+    p.max_seq_len = int(max_seq_len) if max_seq_len else block_table.shape[1] * p.block_size
+    nbytes = prefill_workspace_size(p, num_tokens, split_keys)
+    ws_ptr = None
+    if nbytes:
+        if workspace is None:
+            workspace = _prefill_ws.get(nbytes, query.device)
+        if workspace.numel() * workspace.element_size() < nbytes:
+            raise ValueError(f"workspace smaller than {nbytes} bytes")
+        ws_ptr = workspace.data_ptr()
+    _lib.call("vaa_paged_attention_prefill_split", ctypes.byref(p), query.data_ptr(),
               key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
               token_to_seq.data_ptr(), positions.data_ptr(), output.data_ptr(), num_tokens,
-              _lib.stream_handle(stream))
+              int(split_keys), ws_ptr, nbytes, _lib.stream_handle(stream))
     return output
 
 
