@@ -25,8 +25,9 @@ def _inputs(T, H, I, dtype, seed):
 
 
 @pytest.mark.parametrize("T,H,I", [(1, 64, 128), (3, 128, 128), (37, 192, 256), (5, 320, 128),
-                                   (256, 320, 128), (300, 512, 384), (513, 448, 256),
-                                   (1000, 1024, 512)])
+                                   (70, 256, 128), (128, 320, 256), (100, 5120, 128),
+                                   (129, 256, 128), (256, 320, 128), (300, 512, 384),
+                                   (513, 448, 256), (1000, 1024, 512)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gate_up_silu_vs_oracle(gpu, T, H, I, dtype):
     from vllm_apple_amd import kernels

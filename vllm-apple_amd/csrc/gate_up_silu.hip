@@ -57,6 +57,10 @@ constexpr int kGRowB = kGK * 2;                  // bytes per LDS row
 constexpr int kGTileB = 256 * kGRowB;            // one operand tile: 256 rows, 32 KB
 constexpr int kGLoads = kGTileB / (kGThreads * 16);  // direct loads per wave per operand
 constexpr int kGXcds = 8;
+#ifndef VAA_GLU_SMALL_TOKENS
+#define VAA_GLU_SMALL_TOKENS 128
+#endif
+constexpr int kSmallTokens = VAA_GLU_SMALL_TOKENS;  // the few-token kernel up to this many tokens
 static_assert(kGLoads == 8, "eight 1 KB direct loads per wave and operand");
 
 // Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format,
@@ -270,6 +274,190 @@ gate_up_silu_kernel(GluArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Few tokens (decode-sized batches, T <= 128): the weights are the stream
+// (671 MB at hidden 5120 x 2 x intermediate 32768) and the product is small,
+// so the 256-token tile above spends most of its MFMAs on padding and runs
+// one workgroup per CU.  Here a workgroup owns 64 output columns (64 gate and
+// the 64 up rows of the same columns) and all tokens (TB blocks of 32): its
+// weight tile is 16 KB per 64-element k-step, so two workgroups share a CU
+// and 512 of them cover intermediate 32768.  Tiles move with the same direct
+// loads, swizzled 128-byte LDS rows and counted waits as above; weights go
+// through a ring of three stages (two steps of lookahead), activations
+// through two.  Wave w computes column half c = w & 1 (gate block c and up
+// block 2 + c, 32 rows each).  With an even number of token blocks the
+// other wave bit picks half of them (every k sub-step, epilogue straight from
+// the registers); with one or three, it picks a k half of every step (two of
+// the four 16-element sub-steps) for every token block, the k halves are
+// summed through LDS and waves 0 and 1 apply the SiLU epilogue.
+// Token rows past num_tokens read the last token's row; their outputs are
+// not stored.
+constexpr int kSCols = 64;                    // output columns per workgroup
+constexpr int kSWTile = 2 * kSCols * kGRowB;  // weight tile per k-step: 128 rows, 16 KB
+constexpr int kSWStages = 3;
+
+// s_waitcnt vmcnt(4) lgkmcnt(0): all of this wave's loads but the newest 4
+// (its weight loads of the next step) have landed.
+__device__ __forceinline__ void glu_small_wait() { __builtin_amdgcn_s_waitcnt(0x0074); }
+
+template <typename T, int TB>
+__global__ void __launch_bounds__(kGThreads) gate_up_silu_small_kernel(GluArgs a) {
+  extern __shared__ __align__(16) char smem[];  // W stages, then x stages
+  constexpr int kXTile = TB * 32 * kGRowB;
+  constexpr bool kTokSplit = TB % 2 == 0;   // waves split the token blocks, else the k sub-steps
+  constexpr int NB = kTokSplit ? TB / 2 : TB;  // token blocks per wave
+  constexpr int NS = kTokSplit ? 4 : 2;        // 16-element sub-steps per wave and step
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)));
+  const int i0 = blockIdx.x * kSCols;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+
+  // Loads: weight rows 0-63 are the gate rows i0.., 64-127 the up rows;
+  // wave w loads rows 32w .. 32w + 31 (four 1 KB loads of 8 rows) and the
+  // activation loads w, w + 4, ... of the TB * 4 in a tile.
+  const char* wbase = (wave < 2 ? a.wg : a.wu) + static_cast<int64_t>(i0) * a.ws;
+  const i32x4v wrs = buffer_rsrc(wbase, static_cast<int>(kSCols * a.ws));
+  const i32x4v xrs = buffer_rsrc(a.x, static_cast<int>(a.num_tokens * a.xs));
+  const int rw = 32 * (wave & 1) + (lane >> 3);  // weight row of load 0 within its matrix
+  const int lc = (lane & 7) ^ (rw & 7);
+  const int woff = rw * static_cast<int>(a.ws) + lc * 16;
+  const int wstep = 8 * static_cast<int>(a.ws);
+  int xoff[TB];
+#pragma unroll
+  for (int j = 0; j < TB; ++j) {
+    const int R = 8 * (wave + 4 * j) + (lane >> 3);
+    xoff[j] = min(R, a.num_tokens - 1) * static_cast<int>(a.xs) + lc * 16;
+  }
+  const uint32_t wdst = 1024 * 4 * wave;
+
+  const int l32 = lane & 31, hb = lane >> 5;
+  const int c = wave & 1, kh = wave >> 1;
+  const int b0 = kTokSplit ? kh * NB : 0;  // first token block of this wave
+  int rd[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    rd[s] = l32 * kGRowB + (((4 * hb + (kTokSplit ? s : 2 * kh + s)) ^ (l32 & 7)) << 4);
+
+  f32x16 g[NB], u[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) g[b][r] = u[b][r] = 0.f;
+
+  const int n = a.ksteps;
+  auto load_w = [&](int ks, uint32_t dst) {
+    const int kb = min(ks, n - 1) * kGRowB;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16(wrs, woff, kb + q * wstep, dst + wdst + 1024 * q);
+  };
+  auto load_x = [&](int ks, uint32_t dst) {
+    const int kb = min(ks, n - 1) * kGRowB;
+#pragma unroll
+    for (int j = 0; j < TB; ++j) dma16(xrs, xoff[j], kb, dst + 1024 * (wave + 4 * j));
+  };
+  const uint32_t xlds = lds0 + kSWStages * kSWTile;
+  load_w(0, lds0);
+  load_x(0, xlds);
+  load_w(1, lds0 + kSWTile);
+  for (int ks = 0; ks < n; ++ks) {
+    glu_small_wait();
+    __syncthreads();
+    const char* cw = smem + (ks % kSWStages) * kSWTile;
+    const char* cx = smem + kSWStages * kSWTile + (ks & 1) * kXTile;
+    load_x(ks + 1, xlds + ((ks + 1) & 1) * kXTile);
+    load_w(ks + 2, lds0 + ((ks + 2) % kSWStages) * kSWTile);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4 ag = *reinterpret_cast<const u32x4*>(cw + (32 * c) * kGRowB + rd[s]);
+      const u32x4 au = *reinterpret_cast<const u32x4*>(cw + (kSCols + 32 * c) * kGRowB + rd[s]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const u32x4 bx = *reinterpret_cast<const u32x4*>(cx + (32 * (b0 + b)) * kGRowB + rd[s]);
+        g[b] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, ag),
+                                     __builtin_bit_cast(typename Elem<T>::x8, bx), g[b]);
+        u[b] = Elem<T>::mfma32x32x16(__builtin_bit_cast(typename Elem<T>::x8, au),
+                                     __builtin_bit_cast(typename Elem<T>::x8, bx), u[b]);
+      }
+    }
+  }
+  // Every load has landed and every wave is done with the tiles before the
+  // LDS is reused for the k-half sums.
+  __builtin_amdgcn_s_waitcnt(0x0070);
+  if constexpr (kTokSplit) {
+    // Lane holds token 32(b0 + b) + l32 and, of column half c, columns
+    // 8 (r / 4) + 4 hb + r % 4.
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int tok = 32 * (b0 + b) + l32;
+      if (tok >= a.num_tokens) continue;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        T v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = Elem<T>::from_f(silu_mul1(g[b][4 * r4 + e], u[b][4 * r4 + e]));
+        *reinterpret_cast<u32x2*>(a.out + static_cast<int64_t>(tok) * a.os +
+                                  2 * (i0 + 32 * c + 8 * r4 + 4 * hb)) =
+            __builtin_bit_cast(u32x2, v);
+      }
+    }
+  } else {
+    __syncthreads();
+    constexpr int kVals = 2 * TB * 16;
+    float* part = reinterpret_cast<float*>(smem) + c * kVals * kWave + lane;
+    if (kh == 1) {
+#pragma unroll
+      for (int b = 0; b < TB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          part[(32 * b + r) * kWave] = g[b][r];
+          part[(32 * b + 16 + r) * kWave] = u[b][r];
+        }
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    // Lane holds token 32b + l32 and, of column half c, columns
+    // 8 (r / 4) + 4 hb + r % 4.
+#pragma unroll
+    for (int b = 0; b < TB; ++b) {
+      const int tok = 32 * b + l32;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        T v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * r4 + e;
+          v[e] = Elem<T>::from_f(silu_mul1(g[b][r] + part[(32 * b + r) * kWave],
+                                           u[b][r] + part[(32 * b + 16 + r) * kWave]));
+        }
+        if (tok < a.num_tokens)
+          *reinterpret_cast<u32x2*>(a.out + static_cast<int64_t>(tok) * a.os +
+                                    2 * (i0 + 32 * c + 8 * r4 + 4 * hb)) =
+              __builtin_bit_cast(u32x2, v);
+      }
+    }
+  }
+}
+
+template <typename T, int TB>
+int launch_small(const GluArgs& a, int inter, hipStream_t stream) {
+  const size_t lds = static_cast<size_t>(kSWStages) * kSWTile + 2 * TB * 32 * kGRowB;
+  hipLaunchKernelGGL((gate_up_silu_small_kernel<T, TB>), dim3(inter / kSCols), dim3(kGThreads),
+                     lds, stream, a);
+  return check_launch("gate_up_silu_small_kernel");
+}
+
+template <typename T>
+int launch_gate_up_silu_small(const GluArgs& a, int inter, hipStream_t stream) {
+  switch ((a.num_tokens + 31) / 32) {
+    case 1: return launch_small<T, 1>(a, inter, stream);
+    case 2: return launch_small<T, 2>(a, inter, stream);
+    case 3: return launch_small<T, 3>(a, inter, stream);
+    default: return launch_small<T, 4>(a, inter, stream);
+  }
+}
+
 template <typename T>
 int launch_gate_up_silu(const GluArgs& a0, hipStream_t stream) {
   GluArgs a = a0;
@@ -325,5 +513,8 @@ extern "C" int vaa_gate_up_silu(const uint16_t* x, int64_t x_stride, const uint1
     return fail(VAA_ERR_UNSUPPORTED, "%s: problem too large", what);
   a.tiles = static_cast<int>(tiles);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (num_tokens <= kSmallTokens)
+    return dtype == VAA_DTYPE_F16 ? launch_gate_up_silu_small<f16>(a, intermediate_size, s)
+                                  : launch_gate_up_silu_small<bf16>(a, intermediate_size, s);
   return dtype == VAA_DTYPE_F16 ? launch_gate_up_silu<f16>(a, s) : launch_gate_up_silu<bf16>(a, s);
 }
