@@ -333,6 +333,31 @@ def _copies(nbytes: int, floor: int = 1) -> int:
     return max(floor, -(-300_000_000 // max(1, nbytes)))
 
 
+def _copy_floor(moved_bytes: int, steps: int, warmup: int) -> float:
+    """ms of a plain device copy (torch's copy_) that reads moved_bytes / 2 and
+    writes moved_bytes / 2, timed over a rotation like the ops: the practical
+    HBM floor for one pass of this size.  Below a few hundred MB a pass pays
+    the launch, the first memory latency and the tail of its last wave, so even
+    this copy stays well under the 8 TB/s peak (43 MB: about 54 %)."""
+    import torch
+
+    n = max(1, moved_bytes // 4)  # fp16 elements per copy
+    dev = torch.device("cuda:0")
+    sets = [(torch.empty(n, dtype=torch.float16, device=dev).normal_(),
+             torch.empty(n, dtype=torch.float16, device=dev)) for _ in range(_copies(4 * n))]
+    t = _timed_rot([lambda s=s_: s[1].copy_(s[0]) for s_ in sets], steps, warmup)
+    del sets
+    return t
+
+
+def _vs_copy(t_op: float, moved_bytes: int, steps: int, warmup: int) -> dict:
+    """The copy floor of an op's bytes and the op's time as a fraction of it."""
+    t_c = _copy_floor(moved_bytes, steps, warmup)
+    return {"copy_floor_ms": round(t_c, 5), "copy_floor_pct_hbm_peak":
+            round(100 * moved_bytes / (t_c * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "op_vs_copy_floor": round(t_c / t_op, 3)}
+
+
 def _decode_record(name: str, b, args, partition: int, note: str) -> dict:
     import torch
 
@@ -436,6 +461,7 @@ def wl_c3(args) -> dict:
     rec = {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
             "tokens": T, "kv_write_ms": round(t_kv, 5),
             "kv_write_gb_s": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
+            "kv_write_copy_floor": _vs_copy(t_kv, kv_bytes, args.steps, args.warmup),
             "prefill_ms": round(t_at, 5), "flops": fl,
             "tflop_s": round(fl / (t_at * 1e-3) / 1e12, 1),
             "mfma_util_pct": round(100 * fl / (t_at * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2),
@@ -594,7 +620,8 @@ def wl_c5(args) -> dict:
                       ("silu_mul", t_silu, silu_bytes), ("qkv_epilogue", t_epi, epi_bytes),
                       ("add_rmsnorm", t_addnorm, addnorm_bytes)):
         rec[nm] = {"ms": round(t, 5), "bytes": by, "gb_s": round(by / (t * 1e-3) / 1e9, 1),
-                   "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+                   "pct_hbm_peak": round(100 * by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                   **_vs_copy(t, by, args.steps, args.warmup)}
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_c5(b, args.cpu_seconds,
                                      {"rmsnorm": norm_bytes, "rope": rope_bytes,

@@ -192,32 +192,45 @@ def test_forward_bf16_activations_fp16_cache(gpu):
     assert_close(host(out.float()), ref, atol=2e-3, rtol=1e-2 + 2 ** -8, what="bf16 over fp16")
 
 
-def test_forward_encoder_only_bidirectional(gpu):
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_encoder_only(gpu, causal):
+    """Encoder attention inside each sequence (base_attn.py:223-306): two calls
+    in a row, the second with more tokens (the staging cache grows) and an
+    empty sequence in the middle; every row against torch SDPA in fp32."""
     from vllm_apple_amd.backend import AttentionType, HipAttentionImpl, HipAttentionMetadata
 
     H, KV, D = 8, 2, 64
-    g = torch.Generator().manual_seed(3)
-    lens = [5, 40, 17]
-    T = sum(lens)
-    q = torch.randn(T, H, D, generator=g).half()
-    k = torch.randn(T, KV, D, generator=g).half()
-    v = torch.randn(T, KV, D, generator=g).half()
-    qsl = torch.tensor([0, 5, 45, 62], dtype=torch.int32)
     impl = HipAttentionImpl(H, D, 0.125, KV, None, None, "auto",
                             attn_type=AttentionType.ENCODER_ONLY)
     dev = torch.device("cuda")
-    md = HipAttentionMetadata(T, 40, qsl.to(dev), 40, torch.tensor(lens).to(dev), None, None)
-    out = torch.zeros(T, H, D, dtype=torch.float16, device=dev)
-    impl.forward(None, q.to(dev), k.to(dev), v.to(dev), None, md, output=out)
-    torch.cuda.synchronize()
-    ref = torch.zeros(T, H, D)
-    for s in range(3):
-        a, e = int(qsl[s]), int(qsl[s + 1])
-        qt = q[a:e].float().transpose(0, 1)
-        kt = k[a:e].float().transpose(0, 1).repeat_interleave(4, 0)
-        vt = v[a:e].float().transpose(0, 1).repeat_interleave(4, 0)
-        ref[a:e] = F.scaled_dot_product_attention(qt, kt, vt, scale=0.125).transpose(0, 1)
-    assert_close(host(out), ref.numpy(), what="encoder-only")
+    for seed, lens in ((3, [5, 40, 17]), (4, [70, 0, 33, 129, 1])):
+        print(f"[case] encoder causal={causal} lens={lens}", flush=True)
+        g = torch.Generator().manual_seed(seed)
+        T = sum(lens)
+        q = torch.randn(T, H, D, generator=g).half()
+        k = torch.randn(T, KV, D, generator=g).half()
+        v = torch.randn(T, KV, D, generator=g).half()
+        qsl = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+        md = HipAttentionMetadata(T, max(lens), qsl.to(dev), max(lens),
+                                  torch.tensor(lens).to(dev), None, None)
+        out = torch.zeros(T, H, D, dtype=torch.float16, device=dev)
+        if causal:  # the staging path's causal form (forward passes is_causal=False,
+            # as metal_attn.py:639-647 does)
+            impl._attention_no_cache(q.to(dev), k.to(dev), v.to(dev), out, md, causal=True)
+        else:
+            impl.forward(None, q.to(dev), k.to(dev), v.to(dev), None, md, output=out)
+        torch.cuda.synchronize()
+        ref = torch.zeros(T, H, D)
+        for s_ in range(len(lens)):
+            a, e = int(qsl[s_]), int(qsl[s_ + 1])
+            if e == a:
+                continue
+            qt = q[a:e].float().transpose(0, 1)
+            kt = k[a:e].float().transpose(0, 1).repeat_interleave(4, 0)
+            vt = v[a:e].float().transpose(0, 1).repeat_interleave(4, 0)
+            ref[a:e] = F.scaled_dot_product_attention(qt, kt, vt, scale=0.125,
+                                                      is_causal=causal).transpose(0, 1)
+        assert_close(host(out), ref.numpy(), what=f"encoder-only causal={causal}")
 
 
 def test_engine_ops_planar_qkv_decode_step(gpu):

@@ -187,6 +187,31 @@ def test_split_decodes_and_prefills():
     assert f([0]) == (0, 0, 0, 0)
 
 
+def test_split_decodes_and_prefills_require_uniform():
+    """Hand-worked cases of vLLM's rule with require_uniform=True, the form the
+    reference's builder calls (metal_attn.py:302-308).  Decodes are the leading
+    requests whose query length equals the first one's."""
+    f = backend.split_decodes_and_prefills
+    # Every query at most the threshold of 1: all decodes, whatever the lengths.
+    assert f([0, 1, 1, 2], 1, require_uniform=True) == (3, 0, 2, 0)
+    # A zero-length request after decodes: a prefill under the uniform rule
+    # (its length differs from the first), a decode under the plain one.
+    assert f([0, 1, 2, 2, 7], 1, require_uniform=True) == (2, 2, 2, 5)
+    assert f([0, 1, 2, 2, 7], 1) == (3, 1, 2, 5)
+    # Threshold 4 (speculative decode): uniform keeps only equal lengths.
+    assert f([0, 3, 6, 8, 20], 4, require_uniform=True) == (2, 2, 6, 14)
+    assert f([0, 3, 6, 8, 20], 4) == (3, 1, 8, 12)
+    # With a threshold above 1, all-short batches still split on unequal
+    # lengths under the uniform rule.
+    assert f([0, 3, 6, 8], 4, require_uniform=True) == (2, 1, 6, 2)
+    assert f([0, 3, 6, 8], 4) == (3, 0, 8, 0)
+    # First request longer than the threshold: no decodes.
+    assert f([0, 9, 10], 4, require_uniform=True) == (0, 2, 0, 10)
+    # Mixed 1-token decodes then prefills: both rules agree at threshold 1.
+    for qsl in ([0, 1, 2, 10, 12], [0, 1, 2, 3], [0, 5, 9]):
+        assert f(qsl, 1, require_uniform=True) == f(qsl, 1)
+
+
 def test_metadata_builder():
     cm = SimpleNamespace(num_actual_tokens=12, max_query_len=8,
                          query_start_loc=torch.tensor([0, 1, 2, 10, 12], dtype=torch.int32),

@@ -124,31 +124,69 @@ class HipAttentionMetadata:
         return self._seq_lens_cpu
 
 
-def split_decodes_and_prefills(query_start_loc_cpu: list, decode_threshold: int = 1):
+def split_decodes_and_prefills(query_start_loc_cpu: list, decode_threshold: int = 1,
+                               require_uniform: bool = False):
     """(num_decodes, num_prefills, num_decode_tokens, num_prefill_tokens) for a
     batch whose decode requests come first, as vLLM's reorder guarantees.
 
-    Restates the behaviour of vLLM's split_decodes_and_prefills, which the
-    reference calls (metal_attn.py:302-308); vLLM is not vendored, so this
-    boundary is not pinned by a reference test.
+    Restates vLLM's split_decodes_and_prefills (vllm/v1/attention/backends/
+    utils.py), which the reference calls with require_uniform=True
+    (metal_attn.py:302-308):
+      * every request is a decode when the longest query is at most
+        decode_threshold (with require_uniform only when the threshold is 1);
+      * no decodes when the first request's query is longer than the threshold;
+      * otherwise the decodes are the leading requests up to the first
+        "prefill": a query longer than the threshold, or, with
+        require_uniform, a query whose length differs from the first one's.
+    vLLM is not vendored with the reference, so this boundary is pinned by
+    hand-worked cases only.
     """
     qsl = list(query_start_loc_cpu)
     num_reqs = len(qsl) - 1
     num_tokens = qsl[-1] if qsl else 0
+    if num_reqs <= 0:
+        return 0, 0, 0, 0
     lens = [qsl[i + 1] - qsl[i] for i in range(num_reqs)]
-    first_prefill = next((i for i, n in enumerate(lens) if n > decode_threshold), num_reqs)
-    num_decode_tokens = qsl[first_prefill] if num_reqs else 0
+    if max(lens) <= decode_threshold and (not require_uniform or decode_threshold <= 1):
+        return num_reqs, 0, num_tokens, 0
+    if lens[0] > decode_threshold:
+        return 0, num_reqs, 0, num_tokens
+    if require_uniform:
+        is_prefill = [n != lens[0] for n in lens]
+    else:
+        is_prefill = [n > decode_threshold for n in lens]
+    if not any(is_prefill):
+        return num_reqs, 0, num_tokens, 0
+    first_prefill = is_prefill.index(True)
+    num_decode_tokens = qsl[first_prefill]
     return (first_prefill, num_reqs - first_prefill, num_decode_tokens,
             num_tokens - num_decode_tokens)
 
 
-class HipAttentionMetadataBuilder:
-    """Builds HipAttentionMetadata from vLLM's CommonAttentionMetadata."""
+try:  # pragma: no cover - vLLM is not installed in the build container
+    from vllm.v1.attention.backends.utils import AttentionMetadataBuilder as _VllmBuilder
+except Exception:  # noqa: BLE001
+    _VllmBuilder = None
+
+
+class HipAttentionMetadataBuilder(_VllmBuilder[HipAttentionMetadata]
+                                  if _VllmBuilder is not None else object):
+    """Builds HipAttentionMetadata from vLLM's CommonAttentionMetadata
+    (MetalAttentionMetadataBuilder, metal_attn.py:253-321).  Derives from
+    vLLM's AttentionMetadataBuilder when vLLM is importable."""
 
     reorder_batch_threshold: int = 1
 
     def __init__(self, kv_cache_spec: Any = None, layer_names: Optional[list] = None,
                  vllm_config: Any = None, device: Optional[torch.device] = None):
+        if _VllmBuilder is not None:  # pragma: no cover - needs vLLM
+            super().__init__(kv_cache_spec, layer_names or [], vllm_config, device)
+            init_reorder = getattr(self, "_init_reorder_batch_threshold", None)
+            if init_reorder is not None:
+                init_reorder(1, False)
+        # Decode requests (one query token) are reordered to the front of the
+        # batch, as the reference's builder asks (metal_attn.py:265).
+        self.reorder_batch_threshold = 1
         self.kv_cache_spec = kv_cache_spec
         self.layer_names = layer_names or []
         self.vllm_config = vllm_config
@@ -165,7 +203,7 @@ class HipAttentionMetadataBuilder:
         num_decode_tokens = 0
         if cm.causal:
             _, _, num_decode_tokens, _ = split_decodes_and_prefills(
-                qsl_list, self.reorder_batch_threshold)
+                qsl_list, self.reorder_batch_threshold, require_uniform=True)
         seq_cpu = getattr(cm, "seq_lens_cpu", None)
         return HipAttentionMetadata(
             num_actual_tokens=cm.num_actual_tokens,
@@ -182,6 +220,10 @@ class HipAttentionMetadataBuilder:
             _seq_lens_cpu=seq_cpu.tolist() if isinstance(seq_cpu, torch.Tensor) else seq_cpu,
         )
 
+
+# Staging cache of the no-cache (encoder) path: grow-only, reused by calls
+# ordered on one stream.
+_no_cache_scratch = kernels._GrowOnlyScratch()
 
 OVERLAP_ENV = "VLLM_VAA_OVERLAP"
 
@@ -353,37 +395,36 @@ class HipAttentionImpl(AttentionImpl):
         """
         qsl = attn_metadata.query_start_loc_cpu
         num_seqs = len(qsl) - 1
-        bs = 16
-        blk_off, nblk = [], []
-        total = 0
-        for s in range(num_seqs):
-            n = qsl[s + 1] - qsl[s]
-            blk_off.append(total)
-            nblk.append((n + bs - 1) // bs)
-            total += nblk[-1]
-        T = query.shape[0]
-        if T == 0 or total == 0:
+        T = min(query.shape[0], qsl[-1] if num_seqs > 0 else 0)
+        if T <= 0:
             return output
-        maxb = max(max(nblk), 1)
-        slots, tok, pos = [], [], []
-        bt = [[-1] * maxb for _ in range(num_seqs)]
-        for s in range(num_seqs):
-            n = qsl[s + 1] - qsl[s]
-            for i in range(nblk[s]):
-                bt[s][i] = blk_off[s] + i
-            for i in range(n):
-                slots.append(blk_off[s] * bs + i)
-                tok.append(s)
-                pos.append(i if causal else n - 1)
+        bs = 16
         dev = query.device
+        # Per-sequence tables on the host (num_seqs entries), per-token indices
+        # on the device.
+        start = torch.tensor(qsl[:-1], dtype=torch.int64)
+        lens = torch.tensor(qsl[1:], dtype=torch.int64) - start
+        nblk = (lens + bs - 1) // bs
+        blk_off = torch.cumsum(nblk, 0) - nblk
+        total, maxb = int(nblk.sum()), max(int(nblk.max()), 1)
+        start_d, lens_d, nblk_d, off_d = (t.to(dev, non_blocking=True)
+                                          for t in (start, lens, nblk, blk_off))
+        seq = torch.repeat_interleave(torch.arange(num_seqs, device=dev), lens_d,
+                                      output_size=qsl[-1])[:T]
+        idx = torch.arange(T, device=dev) - start_d[seq]  # index inside the sequence
+        slots = off_d[seq] * bs + idx
+        pos = (idx if causal else lens_d[seq] - 1).to(torch.int32)
+        j = torch.arange(maxb, device=dev)
+        bt = torch.where(j[None, :] < nblk_d[:, None], off_d[:, None] + j[None, :],
+                         torch.full_like(j[None, :], -1)).to(torch.int32)
         kv = key.shape[1]
-        kc = torch.empty((total, bs, kv, self.head_size), dtype=query.dtype, device=dev)
-        vc = torch.empty_like(kc)
-        slot_t = torch.tensor(slots, dtype=torch.int64).to(dev, non_blocking=True)
-        bt_t = torch.tensor(bt, dtype=torch.int32).to(dev, non_blocking=True)
-        tok_t = torch.tensor(tok, dtype=torch.int32).to(dev, non_blocking=True)
-        pos_t = torch.tensor(pos, dtype=torch.int32).to(dev, non_blocking=True)
-        kernels.kv_write_slots(key, value, kc, vc, slot_t[:T], layout="vllm")
-        kernels.paged_prefill(query, kc, vc, bt_t, tok_t[:T], pos_t[:T], scale=self.scale,
-                              layout="vllm", output=output)
+        scratch = _no_cache_scratch.get(2 * total * bs * kv * self.head_size * query.element_size(),
+                                        dev)
+        kc = scratch[:total * bs * kv * self.head_size * query.element_size()].view(
+            query.dtype).view(total, bs, kv, self.head_size)
+        vc = scratch[kc.numel() * query.element_size():2 * kc.numel() * query.element_size()
+                     ].view(query.dtype).view(total, bs, kv, self.head_size)
+        kernels.kv_write_slots(key[:T], value[:T], kc, vc, slots, layout="vllm")
+        kernels.paged_prefill(query[:T], kc, vc, bt, seq.to(torch.int32), pos, scale=self.scale,
+                              layout="vllm", output=output[:T])
         return output
