@@ -144,5 +144,12 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
 __device__ __forceinline__ void st16(void* p, u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
+// 16-byte global load with the nontemporal hint, for data a kernel reads once
+// per call (the decode's K/V stream).  Each load instruction of a wave should
+// cover whole 64-byte pieces: scattered 16-byte pieces under the hint cost
+// more than they save.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 
 }  // namespace vaa

@@ -5,7 +5,9 @@
 // consecutive threads walk a head row, so a wave reads and writes whole
 // 256-byte rows (D = 128) with 16-byte accesses.  The destination of each
 // token comes from a small "resolver" (slot, decode position, or explicit
-// block/offset) that returns false to skip the token.
+// block/offset) that returns false to skip the token.  The new K/V rows are
+// read once, with the nontemporal hint (C3 chunk write 5.90 -> 5.67 us); the
+// cache rows are stored normally, since attention reads them next.
 #include "common.h"
 
 namespace vaa {
@@ -121,8 +123,8 @@ kv_copy_kernel(CacheDst dst, NewSrc src, Resolver resolve, int num_tokens,
     const int64_t dk = block * dst.k_sb + h * dst.k_sh + off * dst.k_st + e;
     const int64_t dv = block * dst.v_sb + h * dst.v_sh + off * dst.v_st + e;
     if constexpr (VEC == 8) {
-      st16(dst.k + dk, ld16(src.k + so));
-      st16(dst.v + dv, ld16(src.v + so));
+      st16(dst.k + dk, ld16_stream(src.k + so));
+      st16(dst.v + dv, ld16_stream(src.v + so));
     } else {
       dst.k[dk] = src.k[so];
       dst.v[dv] = src.v[so];

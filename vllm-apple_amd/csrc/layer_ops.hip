@@ -2,7 +2,9 @@
 // NeoX rotary embedding (in place on Q and K) and SwiGLU (silu(gate) * up).
 // 16-bit in / 16-bit out (fp16, the reference's type, or bf16) with fp32
 // arithmetic; 16-byte vector accesses when the views allow it, 2-byte
-// fallbacks otherwise.
+// fallbacks otherwise.  Rows read once carry the nontemporal hint (C5 on
+// MI355X: RMSNorm 11.9 -> 10.9 us, RoPE 10.8 -> 10.1 us); the norm weights,
+// read by every row, do not.
 #include "common.h"
 
 namespace vaa {
@@ -48,13 +50,13 @@ rmsnorm_vec_kernel(const T* in, T* out, const T* w, T* res, int rows,
   T* r = res ? res + row * res_st : nullptr;
   // The row's values: x, or (kAdd) h = half(x + r), written back to r.
   auto load = [&](int c) {
-    const u32x4 v = ld16(x + 8 * c);
+    const u32x4 v = ld16_stream(x + 8 * c);
     if constexpr (!kAdd) {
       return v;
     } else {
       float f[8], rf[8];
       unpack8<T>(v, f);
-      unpack8<T>(ld16(r + 8 * c), rf);
+      unpack8<T>(ld16_stream(r + 8 * c), rf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] += rf[e];
       const u32x4 h = pack8<T>(f);
@@ -189,8 +191,8 @@ __global__ void __launch_bounds__(256) rope_neox_vec_kernel(RopeArgs<T> a) {
       s[e] = s0[e];
       s[e + 4] = s1[e];
     }
-    unpack8<T>(ld16(x + i0), x0);
-    unpack8<T>(ld16(x + i0 + half), x1);
+    unpack8<T>(ld16_stream(x + i0), x0);
+    unpack8<T>(ld16_stream(x + i0 + half), x1);
     float y0[8], y1[8];
     rope_rotate8(x0, x1, c, s, y0, y1);
     st16(x + i0, pack8<T>(y0));
@@ -233,8 +235,8 @@ silu_mul_vec_kernel(const T* gate, const T* up, T* out, int64_t rows,
        idx < total; idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t r = idx / cpr, c = (idx % cpr) * 8;
     float g[8], u[8], y[8];
-    unpack8<T>(ld16(gate + r * g_st + c), g);
-    unpack8<T>(ld16(up + r * u_st + c), u);
+    unpack8<T>(ld16_stream(gate + r * g_st + c), g);
+    unpack8<T>(ld16_stream(up + r * u_st + c), u);
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = silu_mul1(g[e], u[e]);
     st16(out + r * o_st + c, pack8<T>(y));

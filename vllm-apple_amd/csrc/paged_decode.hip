@@ -38,12 +38,18 @@
 // cross-lane max.
 //
 // Memory: each lane loads 16-byte pieces of one K row straight into the MFMA
-// A-operand registers (the contraction index d is permuted identically in K
-// and Q).  V is loaded with fully coalesced 16-byte loads, stored to a per-wave
-// LDS tile (XOR-swizzled 16-byte chunks) and read back transposed.  Loads run
-// two tiles ahead of the math in a rotated three-buffer pipeline, and the
-// wave's block-table entries sit in a VGPR (one per lane) read with readlane,
-// so the steady-state loop issues no scalar memory loads.
+// A-operand registers.  The contraction index is permuted identically in K
+// and Q: MFMA step s, lane group g holds dims 32s + 8g .. +7, so the four
+// lane groups of one token read 64 contiguous bytes per load instruction.  V
+// is loaded with fully coalesced 16-byte loads, stored to a per-wave LDS tile
+// (XOR-swizzled 16-byte chunks) and read back transposed.  The K/V stream is
+// read once per call, so its loads carry the nontemporal hint (MI355X
+// headline: 72 -> 79 % of HBM peak on one box; the hint on the earlier K lane
+// map, 16-byte pieces 64 bytes apart, had cost 8 points), except in the
+// shared balanced split that runs beside a prefill (issue_tile).  Loads run two tiles
+// ahead of the math in a rotated three-buffer pipeline, and the wave's
+// block-table entries sit in a VGPR (one per lane) read with readlane, so the
+// steady-state loop issues no scalar memory loads.
 #include "common.h"
 
 #include <atomic>
@@ -111,7 +117,7 @@ struct Tile {
 // Per-lane constants of the tile loads and LDS traffic.
 template <int D>
 struct LaneMap {
-  uint32_t koff;               // element offset of this lane's K piece in a tile
+  uint32_t koff;               // element offset of this lane's K piece in a tile (step 0)
   uint32_t voff[Cfg<D>::VLD];  // element offset of V chunk i in a tile
   int vrow[Cfg<D>::VLD];       // tile row of V chunk i
   uint32_t wlds[Cfg<D>::VLD];  // LDS element offset where V chunk i is stored
@@ -132,7 +138,11 @@ __device__ __forceinline__ int64_t window_block(const DecodeArgs& a, int vals, i
   return __builtin_amdgcn_readlane(vals, (j * kTile) / a.block_size - blk0);
 }
 
-template <int D>
+// kStream: loads with the nontemporal hint.  Off for the shared balanced
+// split, which runs beside a concurrent prefill whose K/V tiles live in L2:
+// there the hint cost the C5 attention step 2 % (0.64 against 0.62 ms) while
+// it saves 7 % on the decode alone.
+template <int D, bool kStream = true>
 __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
                                           int64_t vbase, const LaneMap<D>& m,
                                           int64_t phys, int j, Tile<D>& t) {
@@ -141,9 +151,11 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
   const f16* kb = a.kc + kbase + phys * a.k_sb + row0 * a.k_st;
   const f16* vb = a.vc + vbase + phys * a.v_sb + row0 * a.v_st;
 #pragma unroll
-  for (int s = 0; s < Cfg<D>::NS; ++s) t.k[s] = ld16(kb + m.koff + 8 * s);
+  for (int s = 0; s < Cfg<D>::NS; ++s)
+    t.k[s] = kStream ? ld16_stream(kb + m.koff + 32 * s) : ld16(kb + m.koff + 32 * s);
 #pragma unroll
-  for (int i = 0; i < Cfg<D>::VLD; ++i) t.v[i] = ld16(vb + m.voff[i]);
+  for (int i = 0; i < Cfg<D>::VLD; ++i)
+    t.v[i] = kStream ? ld16_stream(vb + m.voff[i]) : ld16(vb + m.voff[i]);
 }
 
 // One tile of math.  valid = number of real tokens in the tile (16 for every
@@ -216,7 +228,7 @@ struct RangeOut {
 // positions: each wave streams a contiguous run of tiles, then the waves
 // combine through LDS.  smem is reused on return only after the trailing
 // barrier, so a workgroup may call this repeatedly.
-template <int D, typename T, int NW = kWaves>
+template <int D, typename T, int NW = kWaves, bool kStream = true>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int qh0, int nh, int L, bool fused,
                                              bool write_new, int t0, int t1, const RangeOut& ro,
@@ -236,7 +248,7 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   const int jm = min(je, special);
 
   LaneMap<D> m;
-  m.koff = c16 * static_cast<uint32_t>(a.k_st) + g * (D / 4);
+  m.koff = c16 * static_cast<uint32_t>(a.k_st) + 8 * g;
 #pragma unroll
   for (int i = 0; i < C::VLD; ++i) {
     const int f = i * kWave + lane;
@@ -253,13 +265,13 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   }
   const int64_t kbase = kvh * a.k_sh, vbase = kvh * a.v_sh;
 
-  // Q^T as the B operand: lane holds Q[head c16][g*D/4 + 8s .. +7].
+  // Q^T as the B operand: lane holds Q[head c16][32s + 8g .. +7] for step s.
   u32x4 qb[C::NS];
   {
     const bool hv = c16 < G;
-    const f16* qp = a.q + seq * a.q_st + (qh0 + (hv ? c16 : 0)) * a.q_sh + g * (D / 4);
+    const f16* qp = a.q + seq * a.q_st + (qh0 + (hv ? c16 : 0)) * a.q_sh + 8 * g;
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) qb[s] = hv ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < C::NS; ++s) qb[s] = hv ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
   T* vt = reinterpret_cast<T*>(smem) + wave * (kTile * D);
@@ -281,20 +293,20 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     const int jl = ce - 1;
     Tile<D> r0, r1, r2;
     int64_t p0 = window_block(a, vals, blk0, cb);
-    issue_tile<D>(a, kbase, vbase, m, p0, cb, r0);
+    issue_tile<D, kStream>(a, kbase, vbase, m, p0, cb, r0);
     int64_t p1 = window_block(a, vals, blk0, min(cb + 1, jl));
-    issue_tile<D>(a, kbase, vbase, m, p1, min(cb + 1, jl), r1);
+    issue_tile<D, kStream>(a, kbase, vbase, m, p1, min(cb + 1, jl), r1);
     int64_t p2;
     int j = cb;
     for (; j + 3 <= ce; j += 3) {
       p2 = window_block(a, vals, blk0, min(j + 2, jl));
-      issue_tile<D>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
+      issue_tile<D, kStream>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
       tile_math<D, T>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
       p0 = window_block(a, vals, blk0, min(j + 3, jl));
-      issue_tile<D>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
+      issue_tile<D, kStream>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
       tile_math<D, T>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
       p1 = window_block(a, vals, blk0, min(j + 4, jl));
-      issue_tile<D>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
+      issue_tile<D, kStream>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
       tile_math<D, T>(m, r2, qb, vt, valid_of(p2), g, a.scale_log2, m_run, l_part, acc);
     }
     // Remainder (0..2 tiles): r0 holds tile j, r1 tile j+1.
@@ -325,13 +337,13 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     Tile<D> t;
     {
       const bool mine = (c16 == new_row) && bvalid;
-      const f16* kp = mine ? a.new_k + seq * a.n_st + kvh * a.n_sh + g * (D / 4)
+      const f16* kp = mine ? a.new_k + seq * a.n_st + kvh * a.n_sh + 8 * g
                            : kb + m.koff;
 #pragma unroll
-      for (int s = 0; s < C::NS; ++s) t.k[s] = ld16(kp + 8 * s);
+      for (int s = 0; s < C::NS; ++s) t.k[s] = ld16(kp + 32 * s);
       if (mine && write_new) {
 #pragma unroll
-        for (int s = 0; s < C::NS; ++s) st16(kb + m.koff + 8 * s, t.k[s]);
+        for (int s = 0; s < C::NS; ++s) st16(kb + m.koff + 32 * s, t.k[s]);
       }
     }
 #pragma unroll
@@ -531,7 +543,7 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(y) * (nc + B) + c + seq) * a.Gc;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T, NW>(a, smem, seq, kvh, qh0, nh, L,
+    decode_range<D, T, NW, NW != kSharedWaves>(a, smem, seq, kvh, qh0, nh, L,
                            a.new_k != nullptr && a.seq_lens[seq] == L, hc == 0, t0, t1, ro,
                            true);
     pos = s0 + t1;
