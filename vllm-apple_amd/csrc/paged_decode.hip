@@ -45,8 +45,8 @@
 // (XOR-swizzled 16-byte chunks) and read back transposed.  The K/V stream is
 // read once per call, so its loads carry the nontemporal hint (MI355X
 // headline: 72 -> 79 % of HBM peak on one box; the hint on the earlier K lane
-// map, 16-byte pieces 64 bytes apart, had cost 8 points), except in the
-// shared balanced split that runs beside a prefill (issue_tile).  Loads run two tiles
+// map, 16-byte pieces 64 bytes apart, had cost 8 points); the shared
+// balanced split, which runs beside a prefill, hints V only (issue_tile).  Loads run two tiles
 // ahead of the math in a rotated three-buffer pipeline, and the wave's
 // block-table entries sit in a VGPR (one per lane) read with readlane, so the
 // steady-state loop issues no scalar memory loads.
@@ -138,10 +138,12 @@ __device__ __forceinline__ int64_t window_block(const DecodeArgs& a, int vals, i
   return __builtin_amdgcn_readlane(vals, (j * kTile) / a.block_size - blk0);
 }
 
-// kStream: loads with the nontemporal hint.  Off for the shared balanced
-// split, which runs beside a concurrent prefill whose K/V tiles live in L2:
-// there the hint cost the C5 attention step 2 % (0.64 against 0.62 ms) while
-// it saves 7 % on the decode alone.
+// V rows always load with the nontemporal hint; K rows too when kStream.
+// kStream is off for the shared balanced split, which runs beside a
+// concurrent prefill: there the hint on K cost the C5 attention step 3 %
+// (0.638-0.642 against 0.610-0.612 ms with V alone hinted), while on the
+// decode alone it helps (headline 78.4-78.7 % with V alone, 78.8-79.1 % with
+// both, one box).
 template <int D, bool kStream = true>
 __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
                                           int64_t vbase, const LaneMap<D>& m,
@@ -154,8 +156,7 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
   for (int s = 0; s < Cfg<D>::NS; ++s)
     t.k[s] = kStream ? ld16_stream(kb + m.koff + 32 * s) : ld16(kb + m.koff + 32 * s);
 #pragma unroll
-  for (int i = 0; i < Cfg<D>::VLD; ++i)
-    t.v[i] = kStream ? ld16_stream(vb + m.voff[i]) : ld16(vb + m.voff[i]);
+  for (int i = 0; i < Cfg<D>::VLD; ++i) t.v[i] = ld16_stream(vb + m.voff[i]);
 }
 
 // One tile of math.  valid = number of real tokens in the tile (16 for every
