@@ -19,6 +19,8 @@ def test_engine_mlp_supported_forms():
                                    "activation": "silu", "bias": False}
     assert m.get_output_size(3) == 3 * 256 * 2
     assert m.get_intermediate_size(3) == 3 * 512 * 2
+    # Up to 1024 tokens the fused kernel; above, the library GEMM + silu_mul.
+    assert EngineMLP.FUSED_MAX_TOKENS == 1024 and m.fused_max_tokens == 1024
 
 
 def test_engine_mlp_missing_weights():

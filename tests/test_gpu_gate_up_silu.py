@@ -151,19 +151,24 @@ def test_gate_up_silu_graph_replays_match_eager(gpu):
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {r}"
 
 
+@pytest.mark.parametrize("library_route", [False, True])
 @pytest.mark.parametrize("fused", [True, False])
-def test_engine_mlp_encode(gpu, fused):
+def test_engine_mlp_encode(gpu, fused, library_route):
     """EngineMLP.encode (mlp.py:170-245): down_proj(silu(gate(x)) * up(x)) on
     (buffer, byte offset) views inside an ENCODE phase, against the oracle's
-    activation rounded to fp16 and an fp64 down projection."""
+    activation rounded to fp16 and an fp64 down projection; through the fused
+    kernel and, above fused_max_tokens, through the library GEMM + silu_mul
+    route (which rounds the products to fp16 first, as the reference does)."""
     from vllm_apple_amd.engine import EngineMLP, EngineStepContext
 
-    print(f"[case] EngineMLP fused={fused}", flush=True)
+    print(f"[case] EngineMLP fused={fused} library_route={library_route}", flush=True)
     T, H, I = 37, 256, 512
     x, w = _inputs(T, H, I, torch.float16, 8)
     g = torch.Generator().manual_seed(9)
     down = (torch.randn(H, I, generator=g) / I ** 0.5).half()
     mlp = EngineMLP(None, H, I)
+    if library_route:
+        mlp.fused_max_tokens = 16
     if fused:
         mlp.set_weights(gate_up_proj=w.cuda(), down_proj=down.cuda())
     else:

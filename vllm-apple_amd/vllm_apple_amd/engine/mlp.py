@@ -9,6 +9,12 @@ the down projection is a plain library GEMM (torch.matmul on the step's
 stream).  Weights keep the reference's layouts: gate_proj / up_proj [I, H]
 or the fused gate_up_proj [2I, H] (gate rows first), down_proj [H, I].
 
+Above FUSED_MAX_TOKENS tokens encode takes the reference's order instead: a
+library GEMM into [T, 2I] and kernels.silu_mul over its halves.  On MI355X
+(hidden 5120, intermediate 32768) the fused kernel leads up to 1024 tokens
+(by 9 % at 16-64, 2-5 % at 256-1024) and hipBLASLt's GEMM leads at 2104 and
+4096 tokens (3 and 8 %).
+
 Only the gated SiLU form without biases is on this path; a standard MLP,
 GELU or biases raise NotImplementedError.
 """
@@ -33,6 +39,9 @@ class MLPConfig:
 
 
 class EngineMLP:
+    # Token counts above this run the library GEMM + silu_mul route.
+    FUSED_MAX_TOKENS = 1024
+
     def __init__(self, context: Any, hidden_size: int, intermediate_size: int,
                  gated: bool = True, activation: str = "silu", bias: bool = False):
         if not gated or activation != "silu" or bias:
@@ -47,6 +56,9 @@ class EngineMLP:
         self._fused_gate_up = False
         self._scratch: Optional[torch.Tensor] = None
         self._scratch_streams: set = set()
+        self._gu: Optional[torch.Tensor] = None
+        self._gu_streams: set = set()
+        self.fused_max_tokens = self.FUSED_MAX_TOKENS
 
     def set_weights(self, gate_proj: Optional[torch.Tensor] = None,
                     up_proj: Optional[torch.Tensor] = None,
@@ -73,24 +85,32 @@ class EngineMLP:
             return x
         return x, 0
 
+    def _grow(self, name: str, n: int, like: torch.Tensor,
+              stream: torch.cuda.Stream) -> torch.Tensor:
+        """A scratch of at least n elements kept in attribute `name`,
+        allocated on the stream that writes and reads it, so that when it is
+        outgrown the old block returns to that stream's pool and is reused
+        only by work ordered after the kernels still using it.  A scratch
+        first made on another stream is marked as used on this one
+        (record_stream) before it can be freed."""
+        buf, streams = getattr(self, name), getattr(self, name + "_streams")
+        if buf is None or buf.numel() < n or buf.dtype != like.dtype or buf.device != like.device:
+            setattr(self, name, None)
+            with torch.cuda.stream(stream):
+                buf = torch.empty(n, dtype=like.dtype, device=like.device)
+            setattr(self, name, buf)
+            setattr(self, name + "_streams", {stream.cuda_stream})
+        elif stream.cuda_stream not in streams:
+            buf.record_stream(stream)
+            streams.add(stream.cuda_stream)
+        return buf
+
     def _intermediate(self, num_tokens: int, like: torch.Tensor,
                       stream: torch.cuda.Stream) -> torch.Tensor:
-        """The activated [T, I] scratch, allocated on the stream that writes
-        and reads it, so that when it is outgrown the old block returns to
-        that stream's pool and is reused only by work ordered after the
-        kernels still using it.  A scratch first made on another stream is
-        marked as used on this one (record_stream) before it can be freed."""
+        """The activated [T, I] scratch."""
         n = num_tokens * self.config.intermediate_size
-        if (self._scratch is None or self._scratch.numel() < n
-                or self._scratch.dtype != like.dtype or self._scratch.device != like.device):
-            self._scratch = None
-            with torch.cuda.stream(stream):
-                self._scratch = torch.empty(n, dtype=like.dtype, device=like.device)
-            self._scratch_streams = {stream.cuda_stream}
-        elif stream.cuda_stream not in self._scratch_streams:
-            self._scratch.record_stream(stream)
-            self._scratch_streams.add(stream.cuda_stream)
-        return self._scratch[:n].view(num_tokens, self.config.intermediate_size)
+        return self._grow("_scratch", n, like, stream)[:n].view(num_tokens,
+                                                                self.config.intermediate_size)
 
     def encode(self, step_ctx: Any, hidden_states: Any, output_buffer: Any, num_tokens: int,
                intermediate_buffer: Optional[Any] = None) -> None:
@@ -113,10 +133,22 @@ class EngineMLP:
         else:
             act = self._intermediate(num_tokens, x, s)
         with torch.cuda.stream(s):
-            if self._fused_gate_up:
-                kernels.gate_up_silu(x, self._gate_up_proj, out=act, stream=s)
+            if num_tokens <= self.fused_max_tokens:
+                if self._fused_gate_up:
+                    kernels.gate_up_silu(x, self._gate_up_proj, out=act, stream=s)
+                else:
+                    kernels.gate_up_silu(x, self._gate_proj, self._up_proj, out=act, stream=s)
             else:
-                kernels.gate_up_silu(x, self._gate_proj, self._up_proj, out=act, stream=s)
+                # The reference's order (mlp.py:247-330): both GEMMs into one
+                # [T, 2I] scratch, then silu_mul over its halves.
+                gu = self._grow("_gu", 2 * num_tokens * I, x, s)[:2 * num_tokens * I]
+                gu = gu.view(num_tokens, 2 * I)
+                if self._fused_gate_up:
+                    torch.matmul(x, self._gate_up_proj.t(), out=gu)
+                else:
+                    torch.matmul(x, self._gate_proj.t(), out=gu[:, :I])
+                    torch.matmul(x, self._up_proj.t(), out=gu[:, I:])
+                kernels.silu_mul(gu[:, :I], gu[:, I:], out=act, stream=s)
             torch.matmul(act, self._down_proj.t(), out=out)
 
     def get_intermediate_size(self, num_tokens: int) -> int:
