@@ -55,3 +55,19 @@ def test_cpu_env_and_record():
         bench._CPU_ENV = None
     assert rec["cores"] == env["threads"] and rec["kind"] == "port"
     assert rec["host"]["cpu_model"] == env["cpu_model"]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py runs on one GPU: --gpus above 1 exits with status 2 and a JSON
+    line that says so, before touching any device."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(repo / "bench.py"), "--gpus", "2", "--steps", "1",
+                        "--warmup", "0"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
