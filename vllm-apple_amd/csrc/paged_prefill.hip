@@ -23,9 +23,10 @@
 //
 // Memory: K/V tiles move from HBM straight into LDS with the gfx950 direct
 // loads (global_load_lds_dwordx4: lane i of a wave writes LDS bytes
-// [16i, 16i+16) after the wave-uniform base), double-buffered in four
-// distinct LDS arrays so the next tile streams in during this tile's math
-// with no registers, address arithmetic or LDS stores of its own.  Wave w
+// [16i, 16i+16) after the wave-uniform base in M0), double-buffered, so the
+// next tile streams in during this tile's math with no registers, address
+// arithmetic or LDS stores of its own.  The loads are inline asm the compiler
+// does not track; an explicit wait and barrier per tile publish each tile.  Wave w
 // fetches the tile's 16-key group w, which lies inside one cache block.
 // Rows are unpadded; 16-byte chunks are XOR-swizzled by row so that both the
 // K operand reads (ds_read_b128 down 32 rows) and the transposed V^T reads
@@ -48,8 +49,6 @@ constexpr int kMaxPrefillSplits = 1024;  // grid z of the split-K prefill
 static_assert(kKT == 16 * kWavesP, "one 16-key group per wave");
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) const void gbl_void_t;
 
 struct PrefillArgs {
   const f16* q;
@@ -146,6 +145,19 @@ __device__ __forceinline__ typename Elem<T>::x4 lds_tr4(const f16* p) {
 // expcnt 6:4 left at its maximum, lgkmcnt 11:8): every direct load and LDS
 // access of this wave has landed.
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+
+
+// One 16-byte direct load per lane into LDS at lds + 16 * lane, issued as
+// inline asm so that the compiler does not track it: a tracked LDS DMA makes
+// it wait for every outstanding LDS read (lgkmcnt(0)) before any operand use,
+// which defeats the read-ahead.  The explicit wait_all() + barrier at each
+// tile boundary orders the DMA against the reads.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(lds)
+               : "memory", "m0");
+}
 
 // The block-table entries of 64 consecutive blocks sit in one VGPR (one per
 // lane) and are read with readlane, so the tile loop issues no scalar loads.
@@ -251,26 +263,26 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
   }
   char* kdst = reinterpret_cast<char*>(kd) + 1024 * (wave * C::NI);
   char* vdst = reinterpret_cast<char*>(vd) + 1024 * (wave * C::NI);
+  const uint32_t kl0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(kdst)));
+  const uint32_t vl0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(vdst)));
   if (nvalid > 0) {
     const char* kb = kbase + 2 * (mine * a.k_sb + static_cast<int64_t>(row0) * a.k_st);
     const char* vb = vbase + 2 * (mine * a.v_sb + static_cast<int64_t>(row0) * a.v_st);
     if (nvalid == 16) {  // every tile but a sequence's last
 #pragma unroll
       for (int q = 0; q < C::NI; ++q) {
-        __builtin_amdgcn_global_load_lds((gbl_void_t*)(kb + L.koff[q]),
-                                         (lds_void_t*)(kdst + 1024 * q), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((gbl_void_t*)(vb + L.voff[q]),
-                                         (lds_void_t*)(vdst + 1024 * q), 16, 0, 0);
+        dma16(kb + L.koff[q], kl0 + 1024 * q);
+        dma16(vb + L.voff[q], vl0 + 1024 * q);
       }
       return;
     }
 #pragma unroll
     for (int q = 0; q < C::NI; ++q) {
       if (L.row[q] < nvalid) {
-        __builtin_amdgcn_global_load_lds((gbl_void_t*)(kb + L.koff[q]),
-                                         (lds_void_t*)(kdst + 1024 * q), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((gbl_void_t*)(vb + L.voff[q]),
-                                         (lds_void_t*)(vdst + 1024 * q), 16, 0, 0);
+        dma16(kb + L.koff[q], kl0 + 1024 * q);
+        dma16(vb + L.voff[q], vl0 + 1024 * q);
       } else {
         const u32x4 z = {0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
@@ -293,11 +305,12 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
 // of their MFMAs (kKAhead K reads, kVAhead V^T pairs; the first V^T pairs are
 // issued before the softmax, whose VALU work then hides their latency), and
 // scheduling barriers keep the compiler from hoisting every read (which
-// would not fit the register budget of two waves per SIMD).  Six of each
-// fill that budget at D = 128 (253 VGPRs, no scratch) and hide more of the
-// LDS latency than four (C3: 94.5 against 95.7 us); eight spill.
-constexpr int kKAhead = 6;
-constexpr int kVAhead = 6;
+// would not fit the register budget of two waves per SIMD).  With the direct
+// loads untracked (dma16) the compiler waits for each read with a partial
+// lgkmcnt, so four reads ahead hide as much as six (C3 89.3-89.9 against
+// 89.8-90.2 us) in fewer registers (245 VGPRs at D = 128).
+constexpr int kKAhead = 4;
+constexpr int kVAhead = 4;
 
 template <int D, typename T>
 __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, const f16* vt,
@@ -400,9 +413,8 @@ template <int D, typename T>
 __global__ void __launch_bounds__(kThreadsP) __attribute__((amdgpu_waves_per_eu(2, 2)))
 paged_prefill_kernel(PrefillArgs a) {
   using C = PCfg<D>;
-  // Four distinct arrays (not one indexed array) so the compiler can tell the
-  // tile being read from the tile being filled and does not wait for the
-  // in-flight direct loads before every LDS read.
+  // Two K and two V tile buffers; the direct loads into one are ordered
+  // against the reads of the other by the per-tile wait and barrier.
   __shared__ __align__(16) f16 k0s[C::TILE];
   __shared__ __align__(16) f16 k1s[C::TILE];
   __shared__ __align__(16) f16 v0s[C::TILE];
