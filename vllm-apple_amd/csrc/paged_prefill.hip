@@ -587,33 +587,48 @@ paged_prefill_kernel(PrefillArgs a) {
   }
 }
 
-// Log-sum-exp merge of a split row's partials (one workgroup per (token,
-// head), a thread per dimension): out = sum_z 2^(m_z - M) acc_z / sum_z
-// 2^(m_z - M) l_z.  Rows the reference leaves unwritten stay untouched: the
-// same validity rules as the attention kernel, and the abort mark of split 0.
+// Log-sum-exp merge of the split rows' partials: out = sum_z 2^(m_z - M) acc_z /
+// sum_z 2^(m_z - M) l_z with M the largest m_z of a piece that saw keys.  One
+// 256-thread workgroup per token; a thread takes four dimensions of one head at
+// a time, so the token's position is read once and every head's partials load
+// at once (one workgroup per (token, head) spent C5's merge in launch and load
+// latency).  Rows the reference leaves unwritten stay untouched: the same
+// validity rules as the attention kernel, and the abort mark of split 0.
+constexpr int kMergeThreads = 256;
+
 template <int D, typename T>
-__global__ void __launch_bounds__(D) prefill_merge_kernel(PrefillArgs a) {
-  const int tok = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+__global__ void __launch_bounds__(kMergeThreads) prefill_merge_kernel(PrefillArgs a) {
+  const int tok = blockIdx.x;
   const int seq = a.tok_seq[tok], pos = a.pos[tok];
   if (seq < 0 || seq >= a.num_seqs || pos < 0) return;
   if ((static_cast<int64_t>(pos) + a.block_size) / a.block_size > a.max_blocks) return;
   const int rs = row_splits(a, pos);
   if (rs <= 1) return;
-  const int64_t row0 = (static_cast<int64_t>(tok) * a.num_q_heads + head) * a.n_splits;
-  if (a.ws_ml[row0 * 2 + 1] < 0.f) return;  // aborted
-  float M = -INFINITY, num = 0.f, den = 0.f;
-  for (int z = 0; z < rs; ++z) {
-    const float mz = a.ws_ml[(row0 + z) * 2], lz = a.ws_ml[(row0 + z) * 2 + 1];
-    if (!(lz > 0.f)) continue;
-    const float az = a.ws_acc[(row0 + z) * D + d];
-    const float Mn = fmaxf(M, mz);
-    const float so = fast_exp2(M - Mn), sn = fast_exp2(mz - Mn);
-    num = num * so + az * sn;
-    den = den * so + lz * sn;
-    M = Mn;
+  constexpr int G4 = D / 4;
+  const int H = a.num_q_heads;
+  for (int it = threadIdx.x; it < H * G4; it += kMergeThreads) {
+    const int head = it / G4, d = (it % G4) * 4;
+    const int64_t row0 = (static_cast<int64_t>(tok) * H + head) * a.n_splits;
+    if (a.ws_ml[row0 * 2 + 1] < 0.f) continue;  // aborted
+    float M = -INFINITY;
+    for (int z = 0; z < rs; ++z)
+      if (a.ws_ml[(row0 + z) * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[(row0 + z) * 2]);
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    if (M != -INFINITY) {
+      for (int z = 0; z < rs; ++z) {
+        const float mz = a.ws_ml[(row0 + z) * 2], lz = a.ws_ml[(row0 + z) * 2 + 1];
+        if (!(lz > 0.f)) continue;
+        const float w = fast_exp2(mz - M);
+        const f32x4 az = *reinterpret_cast<const f32x4*>(a.ws_acc + (row0 + z) * D + d);
+        num += w * az;
+        den += w * lz;
+      }
+    }
+    T* o = reinterpret_cast<T*>(a.out) + static_cast<int64_t>(tok) * a.o_st + head * a.o_sh + d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = Elem<T>::from_f(den > 0.f ? num[e] / den : 0.f);
   }
-  reinterpret_cast<T*>(a.out)[static_cast<int64_t>(tok) * a.o_st + head * a.o_sh + d] =
-      Elem<T>::from_f(den > 0.f ? num / den : 0.f);
 }
 
 template <int D, typename T>
@@ -630,7 +645,7 @@ int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   hipLaunchKernelGGL((paged_prefill_kernel<D, T>), grid, dim3(kThreadsP), 0, stream, b);
   const int st = check_launch("paged_prefill_kernel");
   if (st || a.split_tiles <= 0) return st;
-  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(a.num_tokens, a.num_q_heads), dim3(D), 0,
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(a.num_tokens), dim3(kMergeThreads), 0,
                      stream, b);
   return check_launch("prefill_merge_kernel");
 }
