@@ -574,14 +574,41 @@ struct MergeAcc {
   __device__ __forceinline__ float value() const { return den > 0.f ? num / den : 0.f; }
 };
 
+// A thread merges four dimensions: the scale factors of a partition are
+// computed once for its four partial sums, and each partial row is read
+// with 16-byte loads (C4 with 512-token partitions: the merge 17.8 -> 12 us,
+// the step 69.4 -> 70.0 % of HBM peak).
+struct MergeAcc4 {
+  float M = -INFINITY, den = 0.f;
+  f32x4 num = {0.f, 0.f, 0.f, 0.f};
+  __device__ __forceinline__ void add(float mp, float lp, const f32x4& ap) {
+    if (!(lp > 0.f)) return;
+    const float Mn = fmaxf(M, mp);
+    const float so = fast_exp2(M - Mn);  // 0 while M = -inf
+    const float sn = fast_exp2(mp - Mn);
+    num = num * so + ap * sn;
+    den = den * so + lp * sn;
+    M = Mn;
+  }
+};
+
+// Balanced-split merge: a thread takes four dimensions of one query head,
+// kBalMergeRows heads of a sequence per workgroup.
+constexpr int kBalMergeRows = 4;
+
 template <int D, typename T>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(D / 4 * kBalMergeRows)
 paged_decode_merge_balanced_kernel(DecodeArgs a) {
-  const int qh = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+  constexpr int D4 = D / 4;
+  const int qh = blockIdx.x * kBalMergeRows + threadIdx.x / D4, seq = blockIdx.y;
+  const int d4 = threadIdx.x % D4;
+  if (qh >= a.num_q_heads) return;
   const int B = a.num_seqs, nc = a.max_parts;
+  T* o = reinterpret_cast<T*>(a.out) + seq * a.o_st + qh * a.o_sh + 4 * d4;
   const int L = clamped_len(a, seq);
   if (L <= 0) {
-    a.out[seq * a.o_st + qh * a.o_sh + d] = f2h(0.f);  // zero bits in either type
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = Elem<T>::from_f(0.f);
     return;
   }
   const int per = a.ws_hdr[0];
@@ -589,28 +616,32 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
   if (c0 == c1) return;
   const int hg = qh % a.G, y = (qh / a.G) * a.chunks + hg / a.Gc, h = hg % a.Gc;
   const int64_t base = static_cast<int64_t>(y) * (nc + B) + seq;
-  MergeAcc m;
+  MergeAcc4 m;
 #pragma unroll 4
   for (int c = c0; c <= c1; ++c) {
     const int64_t row = (base + c) * a.Gc + h;
-    m.add(a.ws_ml[row * 2], a.ws_ml[row * 2 + 1], a.ws_acc[row * D + d]);
+    m.add(a.ws_ml[row * 2], a.ws_ml[row * 2 + 1],
+          *reinterpret_cast<const f32x4*>(a.ws_acc + row * D + 4 * d4));
   }
-  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(m.value());
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = Elem<T>::from_f(m.den > 0.f ? m.num[i] / m.den : 0.f);
 }
 
 // Second pass for split sequences:
 //   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p,  M = max_p m_p.
-// kMergeSplit thread groups of D threads each merge every kMergeSplit-th
+// kMergeSplit thread groups of D/4 threads each merge every kMergeSplit-th
 // partition (shorter dependent load chains for the long-context split); the
 // group states are then merged the same way through LDS.
 constexpr int kMergeSplit = 4;
 
 template <int D, typename T>
-__global__ void __launch_bounds__(D* kMergeSplit)
+__global__ void __launch_bounds__(D / 4 * kMergeSplit)
 paged_decode_merge_kernel(DecodeArgs a) {
-  __shared__ float st[kMergeSplit][3][D];
+  constexpr int D4 = D / 4;
+  __shared__ float sml[kMergeSplit][2];
+  __shared__ f32x4 snum[kMergeSplit][D4];
   const int qh = blockIdx.x, seq = blockIdx.y;
-  const int d = threadIdx.x % D, grp = threadIdx.x / D;
+  const int d4 = threadIdx.x % D4, grp = threadIdx.x / D4;
   int L = a.seq_lens[seq];
   const int cap = a.max_blocks * a.block_size;
   if (L > cap) L = cap;
@@ -619,19 +650,24 @@ paged_decode_merge_kernel(DecodeArgs a) {
   const int n_parts = min((L + part_tok - 1) / part_tok, a.max_parts);
   if (n_parts <= 1) return;  // written directly by the decode kernel
   const int64_t row0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh) * a.max_parts;
-  MergeAcc m;
+  MergeAcc4 m;
 #pragma unroll 4
   for (int p = grp; p < n_parts; p += kMergeSplit)
-    m.add(a.ws_ml[(row0 + p) * 2], a.ws_ml[(row0 + p) * 2 + 1], a.ws_acc[(row0 + p) * D + d]);
-  st[grp][0][d] = m.M;
-  st[grp][1][d] = m.den;
-  st[grp][2][d] = m.num;
+    m.add(a.ws_ml[(row0 + p) * 2], a.ws_ml[(row0 + p) * 2 + 1],
+          *reinterpret_cast<const f32x4*>(a.ws_acc + (row0 + p) * D + 4 * d4));
+  if (d4 == 0) {
+    sml[grp][0] = m.M;
+    sml[grp][1] = m.den;
+  }
+  snum[grp][d4] = m.num;
   __syncthreads();
   if (grp != 0) return;
-  MergeAcc t;
+  MergeAcc4 t;
 #pragma unroll
-  for (int g = 0; g < kMergeSplit; ++g) t.add(st[g][0][d], st[g][1][d], st[g][2][d]);
-  reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] = Elem<T>::from_f(t.value());
+  for (int g = 0; g < kMergeSplit; ++g) t.add(sml[g][0], sml[g][1], snum[g][d4]);
+  T* o = reinterpret_cast<T*>(a.out) + seq * a.o_st + qh * a.o_sh + 4 * d4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = Elem<T>::from_f(t.den > 0.f ? t.num[i] / t.den : 0.f);
 }
 
 // Merge of caller-supplied attention states (vaa_merge_attn_states): row
@@ -842,8 +878,9 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
                          stream, a);
     int st = check_launch("paged_decode_balanced_kernel");
     if (st) return st;
-    hipLaunchKernelGGL((paged_decode_merge_balanced_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs),
-                       dim3(D), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_merge_balanced_kernel<D, T>),
+                       dim3((a.num_q_heads + kBalMergeRows - 1) / kBalMergeRows, a.num_seqs),
+                       dim3(D / 4 * kBalMergeRows), 0, stream, a);
     return check_launch("paged_decode_merge_balanced_kernel");
   }
   dim3 grid(a.num_kv_heads * a.chunks, a.max_parts, a.num_seqs);
@@ -861,7 +898,7 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
   int st = check_launch("paged_decode_kernel");
   if (st || a.max_parts <= 1) return st;
   hipLaunchKernelGGL((paged_decode_merge_kernel<D, T>), dim3(a.num_q_heads, a.num_seqs),
-                     dim3(D * kMergeSplit), 0, stream, a);
+                     dim3(D / 4 * kMergeSplit), 0, stream, a);
   return check_launch("paged_decode_merge_kernel");
 }
 
