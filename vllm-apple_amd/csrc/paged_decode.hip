@@ -632,7 +632,7 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
 // kMergeSplit thread groups of D/4 threads each merge every kMergeSplit-th
 // partition (shorter dependent load chains for the long-context split); the
 // group states are then merged the same way through LDS.
-constexpr int kMergeSplit = 4;
+constexpr int kMergeSplit = 8;
 
 template <int D, typename T>
 __global__ void __launch_bounds__(D / 4 * kMergeSplit)
