@@ -34,11 +34,12 @@ def test_topk_random_rows(gpu, V, k, dtype):
 
 
 def test_topk_many_rows_one_chunk_each(gpu):
-    """A batch that fills the GPU with one workgroup per row (no workspace,
-    no merge launch), including rows shorter than the register slices."""
+    """A batch that fills the GPU with one workgroup (or, with 4096 rows and
+    more at k <= 64, one wave) per row: no workspace, no merge launch,
+    including rows shorter than the register slices."""
     from vllm_apple_amd import kernels
 
-    for T, V, k in ((1500, 3000, 50), (1100, 4096, 256), (2000, 77, 5)):
+    for T, V, k in ((1500, 3000, 50), (1100, 4096, 256), (2000, 77, 5), (5000, 3000, 50)):
         print(f"[case] topk one-chunk T={T} V={V} k={k}", flush=True)
         assert kernels.topk_workspace_size(T, V, k) == 0
         g = torch.Generator().manual_seed(T)
@@ -119,3 +120,29 @@ def test_engine_topk_encode_and_reconstruct(gpu, monkeypatch):
     keep.scatter_(1, torch.from_numpy(ref_idx).long(), True)
     assert torch.equal(full[keep], logits[keep])
     assert torch.all(torch.isneginf(full[~keep]))
+
+
+@pytest.mark.parametrize("T,k", [(256, 50), (32, 64), (40, 1)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_topk_bench_shape_one_wave_paths(gpu, T, k, dtype):
+    """The bench's vocabulary (128256) at k <= 64, where each chunk and each
+    row's merge runs on one wave: every row against the oracle, with some rows
+    flat or tied so that the chunk and merge lists overflow and take the
+    exact-key and ordered-compaction paths."""
+    from vllm_apple_amd import kernels
+
+    print(f"[case] topk bench shape T={T} k={k} {dtype}", flush=True)
+    V = 128256
+    g = torch.Generator().manual_seed(T * 1000 + k)
+    logits = (torch.randn(T, V, generator=g) * 4).to(dtype)
+    logits[1] = 0.5                                   # flat row: ties everywhere
+    logits[2] = torch.randint(-2, 3, (V,), generator=g).to(dtype)  # five distinct values
+    logits[3, ::97] = float("inf")                    # many equal maxima
+    logits[4] = -float("inf")
+    logits[4, 5000:5000 + 3] = 1.0
+    assert kernels.topk_workspace_size(T, V, k) > 0   # chunked: the merge runs
+    idx, vals = kernels.topk_logits(logits.cuda(), k)
+    torch.cuda.synchronize()
+    ref_idx, ref_vals = otk.topk(_bits(logits), k)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    assert np.array_equal(_bits(vals), ref_vals)
