@@ -63,7 +63,7 @@ enum { VAA_DTYPE_F16 = 0, VAA_DTYPE_BF16 = 1 };
  *        of the 16-token tiles of all sequences, split on the device from
  *        seq_lens (for unequal lengths; at most 8192 sequences).
  *   VAA_PARTITION_BALANCED_SHARED  the same split over workgroups of half the
- *        size, two per CU, for a decode that runs concurrently with another
+ *        size, four per CU, for a decode that runs concurrently with another
  *        kernel (a mixed step's prefill on a second stream): its workgroups
  *        then share CUs with the other kernel's instead of waiting for them.
  *        Slower than VAA_PARTITION_BALANCED when decode runs alone.

@@ -14,11 +14,14 @@
 //              heads, one workgroup each.
 //   block    = 8 waves; each wave streams a contiguous run of 16-token tiles
 //              with its own (max, sum, acc) and the waves are combined in LDS
-//              at the end.  Fixed partitions of at most 1024 tokens and the
-//              shared balanced split (VAA_PARTITION_BALANCED_SHARED) use
+//              at the end.  Fixed partitions of at most 1024 tokens use
 //              4-wave workgroups, two per CU: one's start-up overlaps the
-//              other's streaming, or a concurrent kernel's workgroup takes
-//              the other half of the CU.
+//              other's streaming.  The shared balanced split
+//              (VAA_PARTITION_BALANCED_SHARED), for a decode that runs beside
+//              another kernel, uses 4-wave workgroups too, four per CU's
+//              worth of the split: a concurrent kernel's workgroups hold some
+//              CUs, and the shorter pieces let the dispatcher give the free
+//              CUs more of them.
 //   split-K  = only when the (seq, kv_head) pairs cannot fill the GPU or the
 //              lengths are unequal; partials (max, sum, acc) go to a workspace
 //              and a second kernel merges them (log-sum-exp).  The merge is a
@@ -60,7 +63,9 @@ namespace {
 constexpr int kWaves = 8;   // waves per workgroup
 constexpr int kShortPartTiles = 64;  // fixed partitions up to 1024 tokens run 4-wave workgroups
 constexpr int kSharedWaves = kWaves / 2;  // VAA_PARTITION_BALANCED_SHARED: 4-wave workgroups,
-                                          // two per CU
+constexpr int kSharedPerCu = 4;           // four per CU's worth of the split (C5 step beside
+                                          // the prefill: 3, 4, 6, 8 -> 0.577, 0.571, 0.579,
+                                          // 0.587 ms; two: 0.597)
 constexpr int kTile = 16;   // tokens per MFMA tile
 
 // Tensors are raw 16-bit storage; the kernels' element type T (fp16 or bf16)
@@ -743,7 +748,7 @@ inline int heads_per_chunk(int G) {
 // How a call splits its sequences.
 struct Split {
   bool balanced;     // balanced split over the actual lengths
-  bool shared;       // balanced over 4-wave workgroups, two per CU
+  bool shared;       // balanced over 4-wave workgroups, kSharedPerCu per CU
   int part;          // fixed: tokens per partition (balanced: -1)
   int max_parts;     // fixed: partitions per sequence; balanced: workgroups per kv head
                      // and head chunk
@@ -771,7 +776,7 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
       return fail(VAA_ERR_UNSUPPORTED, "balanced split: num_seqs=%d > %d", p->num_seqs,
                   kBalMaxSeqs);
     const bool shared = part == VAA_PARTITION_BALANCED_SHARED;
-    const int per_cu = shared ? kWaves / kSharedWaves : 1;
+    const int per_cu = shared ? kSharedPerCu : 1;
     const int ys = p->num_kv_heads * head_chunks(p->queries_per_kv);
     const int wgs = (per_cu * num_cus() + ys - 1) / ys;
     sp->balanced = true;

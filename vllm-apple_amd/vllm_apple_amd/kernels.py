@@ -403,7 +403,8 @@ def paged_decode(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torc
     partition_size PARTITION_BALANCED splits by the lengths on the device.
     shared=True says the launch runs concurrently with another kernel (see
     overlap): an automatic balanced split then uses PARTITION_BALANCED_SHARED,
-    two half-size workgroups per CU that share CUs with the other kernel.
+    half-size workgroups, four per CU's worth of the split, that share CUs
+    with the other kernel.
     """
     _require_gpu(query, key_cache, value_cache, block_table, seq_lens, output, new_keys, new_values)
     dt = _attn_dtype(query=query, key_cache=key_cache, value_cache=value_cache, output=output,
