@@ -392,6 +392,9 @@ __global__ void __launch_bounds__(kTkThreads) topk_chunk_kernel(TopkArgs a) {
 //            top k are all >= L;
 //   list     the real items >= L go to the wave's LDS list at offsets from a
 //            wave scan of per-lane counts;
+//   cut      a list of 65 to 128 words (the usual case on logits) is cut at
+//            the exact k-th key among its words, bit by bit over the listed
+//            keys, so that the rank below runs over about k words;
 //   rank     each listed word's rank among the listed words is its output
 //            position when < k.
 // When more than kWaveCand items reach L (flat or heavily tied rows), the
