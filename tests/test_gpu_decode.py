@@ -181,7 +181,8 @@ def test_decode_balanced_ragged_batch(gpu, seed, mode):
     """Balanced split over many ragged sequences (empty ones included): every
     piece boundary (inside a sequence, between sequences, across workgroups)
     against the oracle, with the fused write bit-exact.  mode -1 is one
-    8-wave workgroup per CU, -2 (shared) two 4-wave workgroups per CU."""
+    8-wave workgroup per CU, -2 (shared) 4-wave workgroups, four per CU's
+    worth of the split."""
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(0, 3000, (77,), generator=g)
     lens[::9] = 0
