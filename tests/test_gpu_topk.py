@@ -146,3 +146,23 @@ def test_topk_bench_shape_one_wave_paths(gpu, T, k, dtype):
     ref_idx, ref_vals = otk.topk(_bits(logits), k)
     assert np.array_equal(idx.cpu().numpy(), ref_idx)
     assert np.array_equal(_bits(vals), ref_vals)
+
+
+def test_topk_wave_path_ragged_tail_strided(gpu):
+    """The one-wave-per-chunk path on strided rows whose length is not a
+    multiple of 8 (the last chunk's tail is read element by element) and at
+    k = 64, its largest k, with enough rows for the wave kernel."""
+    from vllm_apple_amd import kernels
+
+    T, V, k = 1400, 10001, 64
+    print(f"[case] topk wave tail T={T} V={V} k={k}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    big = (torch.randn(T, V + 7, generator=g) * 3).half()
+    big[:, V - 1] = 30.0          # the tail's last column is every row's maximum
+    big[::5, V - 3:V] = 30.0      # ties inside the tail
+    logits = big.cuda()[:, :V]    # row stride V + 7 = 10008, a multiple of 8
+    idx, vals = kernels.topk_logits(logits, k)
+    torch.cuda.synchronize()
+    ref_idx, ref_vals = otk.topk(_bits(big[:, :V].contiguous()), k)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    assert np.array_equal(_bits(vals), ref_vals)
