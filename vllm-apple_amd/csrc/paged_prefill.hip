@@ -589,12 +589,15 @@ paged_prefill_kernel(PrefillArgs a) {
 
 // Log-sum-exp merge of the split rows' partials: out = sum_z 2^(m_z - M) acc_z /
 // sum_z 2^(m_z - M) l_z with M the largest m_z of a piece that saw keys.  One
-// 256-thread workgroup per token; a thread takes four dimensions of one head at
-// a time, so the token's position is read once and every head's partials load
-// at once (one workgroup per (token, head) spent C5's merge in launch and load
-// latency).  Rows the reference leaves unwritten stay untouched: the same
+// 256-thread workgroup per token; a thread takes four dimensions of one head
+// for each of kMergeItems heads at a time, and walks the pieces once with a
+// running maximum (each piece rescales the sums when it raises it), so the
+// loads of every piece and item are independent and in flight together (a
+// first pass for the maximum put a dependent round trip before the partial
+// loads).  Rows the reference leaves unwritten stay untouched: the same
 // validity rules as the attention kernel, and the abort mark of split 0.
 constexpr int kMergeThreads = 256;
+constexpr int kMergeItems = 4;
 
 template <int D, typename T>
 __global__ void __launch_bounds__(kMergeThreads) prefill_merge_kernel(PrefillArgs a) {
@@ -606,28 +609,47 @@ __global__ void __launch_bounds__(kMergeThreads) prefill_merge_kernel(PrefillArg
   if (rs <= 1) return;
   constexpr int G4 = D / 4;
   const int H = a.num_q_heads;
-  for (int it = threadIdx.x; it < H * G4; it += kMergeThreads) {
-    const int head = it / G4, d = (it % G4) * 4;
-    const int64_t row0 = (static_cast<int64_t>(tok) * H + head) * a.n_splits;
-    if (a.ws_ml[row0 * 2 + 1] < 0.f) continue;  // aborted
-    float M = -INFINITY;
-    for (int z = 0; z < rs; ++z)
-      if (a.ws_ml[(row0 + z) * 2 + 1] > 0.f) M = fmaxf(M, a.ws_ml[(row0 + z) * 2]);
-    f32x4 num = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
-    if (M != -INFINITY) {
-      for (int z = 0; z < rs; ++z) {
-        const float mz = a.ws_ml[(row0 + z) * 2], lz = a.ws_ml[(row0 + z) * 2 + 1];
-        if (!(lz > 0.f)) continue;
-        const float w = fast_exp2(mz - M);
-        const f32x4 az = *reinterpret_cast<const f32x4*>(a.ws_acc + (row0 + z) * D + d);
-        num += w * az;
-        den += w * lz;
+  for (int it0 = threadIdx.x; it0 < H * G4; it0 += kMergeThreads * kMergeItems) {
+    int64_t row0[kMergeItems];
+    float M[kMergeItems], den[kMergeItems];
+    f32x4 num[kMergeItems];
+    bool aborted[kMergeItems];
+#pragma unroll
+    for (int i = 0; i < kMergeItems; ++i) {
+      const int it = min(it0 + i * kMergeThreads, H * G4 - 1);
+      row0[i] = (static_cast<int64_t>(tok) * H + it / G4) * a.n_splits;
+      M[i] = -INFINITY;
+      den[i] = 0.f;
+      num[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      aborted[i] = false;
+    }
+    for (int z = 0; z < rs; ++z) {
+#pragma unroll
+      for (int i = 0; i < kMergeItems; ++i) {
+        const int it = min(it0 + i * kMergeThreads, H * G4 - 1);
+        const int64_t row = row0[i] + z;
+        const float mz = a.ws_ml[row * 2], lz = a.ws_ml[row * 2 + 1];
+        const f32x4 az = *reinterpret_cast<const f32x4*>(a.ws_acc + row * D + (it % G4) * 4);
+        if (z == 0 && lz < 0.f) aborted[i] = true;
+        if (!(lz > 0.f)) continue;  // a piece that saw no keys (max -inf)
+        const float Mn = fmaxf(M[i], mz);
+        const float so = fast_exp2(M[i] - Mn);  // 0 while M = -inf
+        const float sn = fast_exp2(mz - Mn);
+        num[i] = num[i] * so + az * sn;
+        den[i] = den[i] * so + lz * sn;
+        M[i] = Mn;
       }
     }
-    T* o = reinterpret_cast<T*>(a.out) + static_cast<int64_t>(tok) * a.o_st + head * a.o_sh + d;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = Elem<T>::from_f(den > 0.f ? num[e] / den : 0.f);
+    for (int i = 0; i < kMergeItems; ++i) {
+      const int it = it0 + i * kMergeThreads;
+      if (it >= H * G4 || aborted[i]) continue;
+      const int head = it / G4, d = (it % G4) * 4;
+      T* o = reinterpret_cast<T*>(a.out) + static_cast<int64_t>(tok) * a.o_st + head * a.o_sh + d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = Elem<T>::from_f(den[i] > 0.f ? num[i][e] / den[i] : 0.f);
+    }
   }
 }
 
