@@ -34,7 +34,7 @@ def test_topk_random_rows(gpu, V, k, dtype):
 
 
 def test_topk_many_rows_one_chunk_each(gpu):
-    """A batch that fills the GPU with one workgroup (or, with 4096 rows and
+    """A batch that fills the GPU with one workgroup (or, with 2048 rows and
     more at k <= 64, one wave) per row: no workspace, no merge launch,
     including rows shorter than the register slices."""
     from vllm_apple_amd import kernels
@@ -122,7 +122,7 @@ def test_engine_topk_encode_and_reconstruct(gpu, monkeypatch):
     assert torch.all(torch.isneginf(full[~keep]))
 
 
-@pytest.mark.parametrize("T,k", [(256, 50), (32, 64), (40, 1)])
+@pytest.mark.parametrize("T,k", [(256, 50), (64, 50), (32, 64), (40, 1)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_topk_bench_shape_one_wave_paths(gpu, T, k, dtype):
     """The bench's vocabulary (128256) at k <= 64, where each chunk and each

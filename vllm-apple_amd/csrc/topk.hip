@@ -408,9 +408,10 @@ constexpr int kWaveK = kWave;                 // the bound takes the k-th of 64 
 constexpr int kWaveCand = 512;                // list capacity per wave
 // The wave kernel once there are at least this many chunks: below, a wave per
 // chunk leaves the SIMDs too few waves to hide its serial phases (vocab
-// 128256, k = 50: 32 rows 22.6 us against 19.5 with a workgroup per chunk;
-// 256 rows 39.7 against 62.3 us).
-constexpr int kWaveMinWork = 4096;
+// 128256 in 32 chunks, k = 50, wave against workgroup kernel: 32 rows 21.1
+// against 17.7 us; 64 rows 22.5 / 24.6; 128 rows 26.9 / 35.5; 256 rows 38.3 /
+// 59.4; 512 rows 57.3 / 106.2).
+constexpr int kWaveMinWork = 2048;
 
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
