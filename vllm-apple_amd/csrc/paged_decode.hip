@@ -234,11 +234,18 @@ struct RangeOut {
 // positions: each wave streams a contiguous run of tiles, then the waves
 // combine through LDS.  smem is reused on return only after the trailing
 // barrier, so a workgroup may call this repeatedly.
+//
+// pre, when has_pre: the block-table window of blocks 0-63 of seq (lane i:
+// entry i, as load_window gives it), loaded by the caller before the
+// sequence's length arrived; a wave whose tiles all lie in those blocks
+// (contexts up to 64 blocks) reads its physical blocks from it, one
+// dependent global round trip fewer.
 template <int D, typename T, int NW = kWaves, bool kStream = true>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int qh0, int nh, int L, bool fused,
                                              bool write_new, int t0, int t1, const RangeOut& ro,
-                                             bool trailing_barrier) {
+                                             bool trailing_barrier, bool has_pre = false,
+                                             int pre = -1) {
   using C = Cfg<D>;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int c16 = lane & 15, g = lane >> 4;
@@ -289,10 +296,11 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   auto valid_of = [&](int64_t p) { return (p < 0 || p >= a.num_blocks) ? 0 : kTile; };
   // Each chunk covers the tiles of 64 consecutive blocks (one VGPR of
   // block-table entries).
+  const bool in_pre = has_pre && jm * kTile <= kWave * a.block_size;
   for (int cb = jb; cb < jm;) {
-    const int blk0 = (cb * kTile) / a.block_size;
+    const int blk0 = in_pre ? 0 : (cb * kTile) / a.block_size;
     const int ce = min(jm, ((blk0 + kWave) * a.block_size) / kTile);
-    const int vals = load_window(a, seq, blk0, lane);
+    const int vals = in_pre ? pre : load_window(a, seq, blk0, lane);
     // Three rotating tile buffers; loads run two tiles ahead.  Prefetch
     // indices past the chunk are clamped to its last tile (an L2 hit), which
     // keeps the loop free of branches around loads.
@@ -332,7 +340,11 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     const int j = special;
     const int tok0 = j * kTile;
     const int bi = tok0 / a.block_size;
-    int64_t phys = bi < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi] : -1;
+    int64_t phys;
+    if (has_pre && bi < kWave)
+      phys = __builtin_amdgcn_readlane(pre, bi);  // -1 past max_blocks, as the table read
+    else
+      phys = bi < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi] : -1;
     const bool bvalid = phys >= 0 && phys < a.num_blocks;
     const int valid = bvalid ? min(kTile, L - tok0) : 0;
     if (!bvalid) phys = 0;
@@ -449,6 +461,9 @@ paged_decode_kernel(DecodeArgs a) {
   const int part = blockIdx.y, seq = blockIdx.z;
   const int kvh = blockIdx.x / a.chunks, hc = blockIdx.x % a.chunks;
   const int qh0 = kvh * a.G + hc * a.Gc, nh = min(a.Gc, a.G - hc * a.Gc);
+  // The first partition's window, issued before the length is known
+  // (independent loads, one round trip); later partitions start past it.
+  const int pre = part == 0 ? load_window(a, seq, 0, static_cast<int>(threadIdx.x % kWave)) : -1;
   const int Lorig = a.seq_lens[seq];
   const int L = clamped_len(a, seq);
   if (L <= 0) {
@@ -466,7 +481,8 @@ paged_decode_kernel(DecodeArgs a) {
   ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh0) * a.max_parts + part;
   ro.prow_step = a.max_parts;
   decode_range<D, T, NW>(a, smem, seq, kvh, qh0, nh, L,
-                         a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro, false);
+                         a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro, false, part == 0,
+                         pre);
 }
 
 // Balanced split: the tiles of all sequences (for one kv head) are laid end
