@@ -304,6 +304,11 @@ def test_wide_groups_and_merge_arguments(lib):
     assert st == _lib.VAA_ERR_UNSUPPORTED
     assert lib.vaa_merge_attn_states(None, None, None, 0, 4, 4, 128, None, 0, 0, None, 0,
                                      None) == 0
+    # num_seqs is the grid's y dimension (at most 65535); num_heads (x) may be large.
+    buf0 = ctypes.create_string_buffer(16)
+    a0 = ctypes.addressof(buf0)
+    st = lib.vaa_merge_attn_states(a0, a0, None, 65536, 4, 4, 128, a0, 0, 0, None, 0, None)
+    assert st == _lib.VAA_ERR_UNSUPPORTED and "num_seqs=65536" in _lib.last_error()
     buf = ctypes.create_string_buffer(64)
     a = ctypes.addressof(buf)
     # kernel layout, KV 2, bs 16, D 64: offsets 0..15 are inside a block.

@@ -157,15 +157,36 @@ def _impl(**kw):
     return backend.HipAttentionImpl(**args)
 
 
+def test_sliding_window_rules(monkeypatch):
+    """A window is accepted only where attending over the whole context gives
+    the same result: no context longer than the window.  With max_model_len
+    known, a shorter window is refused at construction; without it, each
+    step's longest context is checked in forward."""
+    monkeypatch.setattr(backend, "_max_model_len", lambda: 4096)
+    with pytest.raises(NotImplementedError, match="sliding_window"):
+        _impl(sliding_window=2048)
+    impl = _impl(sliding_window=4096)
+    assert impl.sliding_window == (-1, -1) and impl._window is None
+    monkeypatch.setattr(backend, "_max_model_len", lambda: None)
+    impl = _impl(sliding_window=4096)
+    assert impl._window == 4096
+    q = torch.zeros(2, 32, 128, dtype=torch.float16)
+    out = torch.ones_like(q)
+    md = backend.HipAttentionMetadata(
+        num_actual_tokens=2, max_query_len=1, query_start_loc=torch.tensor([0, 1, 2]),
+        max_seq_len=4097, seq_lens=torch.tensor([4097, 10]), block_table=torch.zeros(2, 1),
+        slot_mapping=torch.zeros(2), num_decode_tokens=2)
+    with pytest.raises(NotImplementedError, match="exceeds sliding_window=4096"):
+        impl.forward(None, q, q[:, :8], q[:, :8], None, md, output=out)
+    with pytest.raises(NotImplementedError):
+        _impl(sliding_window=0)
+
+
 def test_impl_error_conventions():
     with pytest.raises(NotImplementedError, match="FP8"):
         _impl(kv_cache_dtype="fp8")
     with pytest.raises(ValueError):
         _impl(head_size=80)
-    # A sliding window would be ignored by the kernels: refused, not silently
-    # attended over the whole context.
-    with pytest.raises(NotImplementedError, match="sliding_window"):
-        _impl(sliding_window=4096)
     impl = _impl()
     assert impl.sliding_window == (-1, -1)
     q = torch.zeros(2, 32, 128, dtype=torch.float16)
@@ -270,3 +291,36 @@ def test_prefill_split_choice():
     assert K.choose_prefill_split([16000, 500], [0, 0], 8, 32, 256) == 0
     # short contexts never split
     assert K.choose_prefill_split([2000, 100], [64, 64], 8, 32, 256) == 0
+
+
+def test_prefill_split_workspace_is_bounded():
+    """One 256-token chunk at a 128k context beside 31 short 248-token
+    prefills: the share-based piece (10240 keys, 13 pieces over 7944 tokens)
+    would need 1.72 GB of partials.  The pieces grow until the workspace the
+    kernel asks for (counted over the longest prefill context) fits the cap."""
+    from vllm_apple_amd import _lib, kernels as K
+
+    K._prefill_split_cache.clear()
+    ctx = [131072] + [248] * 31
+    ql = [256] + [248] * 31
+    cap = K.PREFILL_SPLIT_MAX_WORKSPACE
+    sp = K.choose_prefill_split(ctx, ql, 8, 32, 256)
+    assert sp > 0 and sp % 1024 == 0
+    tokens = sum(ql)
+    pieces = -(-131072 // sp)
+    need = tokens * 32 * pieces * 130 * 4
+    assert pieces >= 2 and need <= cap
+    # The library's own sizing agrees when max_seq_len is the longest prefill
+    # context.
+    p = _lib.VaaAttnParams()
+    p.head_size, p.block_size, p.num_kv_heads, p.num_query_heads = 128, 16, 8, 32
+    p.queries_per_kv, p.num_seqs, p.max_blocks_per_seq, p.num_blocks = 4, 32, 8192, 1 << 16
+    p.max_seq_len = 131072
+    assert K.prefill_workspace_size(p, tokens, sp) == need
+    # Without the cap the piece count would be the share-based one.
+    K._prefill_split_cache.clear()
+    free = K.choose_prefill_split(ctx, ql, 8, 32, 256, max_workspace_bytes=1 << 40)
+    assert free < sp and tokens * 32 * -(-131072 // free) * 130 * 4 > cap
+    # A cap too small for two pieces drops the split.
+    K._prefill_split_cache.clear()
+    assert K.choose_prefill_split(ctx, ql, 8, 32, 256, max_workspace_bytes=1 << 20) == 0

@@ -1137,8 +1137,11 @@ extern "C" int vaa_merge_attn_states(const float* partial_out, const float* part
   if (num_seqs == 0) return VAA_OK;
   if (!partial_out || !partial_lse || !output)
     return fail(VAA_ERR_INVALID_ARG, "vaa_merge_attn_states: null pointer");
-  if (o_stride_token < 0 || o_stride_head < 0 || num_heads > 65535)
-    return fail(VAA_ERR_INVALID_ARG, "vaa_merge_attn_states: bad output strides or heads");
+  if (o_stride_token < 0 || o_stride_head < 0)
+    return fail(VAA_ERR_INVALID_ARG, "vaa_merge_attn_states: bad output strides");
+  // Grid (num_heads, num_seqs): y is limited to 65535.
+  if (num_seqs > 65535)
+    return fail(VAA_ERR_UNSUPPORTED, "vaa_merge_attn_states: num_seqs=%d > 65535", num_seqs);
   StatesArgs a;
   a.part_out = partial_out;
   a.part_lse = partial_lse;

@@ -47,6 +47,16 @@ SUPPORTED_HEAD_SIZES = [32, 64, 96, 128]
 BACKEND_NAME = "VAA_HIP_ATTN"
 
 
+def _max_model_len() -> Optional[int]:
+    """vLLM's max_model_len for the model being built, or None without vLLM
+    (or outside a vLLM config context)."""
+    try:  # pragma: no cover - vLLM is not installed in the build container
+        from vllm.config import get_current_vllm_config
+        return int(get_current_vllm_config().model_config.max_model_len)
+    except Exception:  # noqa: BLE001
+        return None
+
+
 def is_quantized_kv_cache(kv_cache_dtype: str) -> bool:
     return kv_cache_dtype not in ("auto", "float16", "half", "fp16", "bfloat16", "bf16")
 
@@ -254,14 +264,23 @@ class HipAttentionImpl(AttentionImpl):
         if alibi_slopes is not None:
             logger.warning("%s does not support ALiBi slopes, ignoring", BACKEND_NAME)
         self.alibi_slopes = None
-        # The kernels attend over the whole context.  The reference keeps the
-        # window and ignores it (metal_attn.py:377-382); a layer with a window
-        # (Mistral-7B-v0.1, Gemma-2/3, Qwen2 SWA layers) would then silently
-        # attend too far, so it is refused here instead.
+        # The kernels attend over the whole context.  A window of W keys
+        # (vLLM's: query position p sees keys p-W+1 .. p) gives the same result
+        # whenever no context is longer than W.  The reference keeps the window
+        # and ignores it (metal_attn.py:377-382), which attends too far once a
+        # context outgrows it; here a window shorter than the model's longest
+        # context (vLLM's max_model_len) is refused, and when that length is
+        # unknown every step's longest context is checked in forward.
+        self._window: Optional[int] = None
         if sliding_window is not None:
-            raise NotImplementedError(
-                f"sliding_window={sliding_window} is not supported by {BACKEND_NAME}: "
-                "the kernels attend over the whole context")
+            window = int(sliding_window)
+            mml = _max_model_len()
+            if window <= 0 or (mml is not None and window < mml):
+                raise NotImplementedError(
+                    f"sliding_window={sliding_window} is not supported by {BACKEND_NAME}: "
+                    f"the kernels attend over the whole context (max_model_len={mml})")
+            if mml is None:
+                self._window = window
         self.sliding_window = (-1, -1)
         self.kv_cache_dtype = kv_cache_dtype
         self.num_queries_per_kv = num_heads // num_kv_heads
@@ -305,6 +324,10 @@ class HipAttentionImpl(AttentionImpl):
                 "Fused output quantization is not yet supported for HipAttentionImpl")
         if attn_metadata is None:  # warm-up / profiling
             return output
+        if self._window is not None and attn_metadata.max_seq_len > self._window:
+            raise NotImplementedError(
+                f"a context of {attn_metadata.max_seq_len} tokens exceeds "
+                f"sliding_window={self._window}: {BACKEND_NAME} attends over the whole context")
 
         # The kernels run in the cache's element type (fp16 or bf16).  Only
         # activations of another type are converted, as the Metal backend
@@ -351,19 +374,21 @@ class HipAttentionImpl(AttentionImpl):
                 # prefill: next to a decode the unsplit prefill is better (its
                 # long workgroups hold a few CUs and leave the rest to the
                 # decode; C5 attention step 0.61 ms against 0.68-0.79 split).
-                split = 0
+                # The pieces are counted over the longest prefill context
+                # (decode contexts do not matter), which bounds the workspace.
+                split, longest = 0, 0
                 lens_host = attn_metadata._seq_lens_cpu
                 qsl_host = attn_metadata._query_start_loc_cpu
                 if lens_host and qsl_host and not overlapped:
-                    pl = [b - a for a, b in zip(qsl_host[:-1], qsl_host[1:])]
+                    ql = [b - a if b - a > 1 else 0 for a, b in zip(qsl_host[:-1], qsl_host[1:])]
                     split = kernels.choose_prefill_split(
-                        lens_host, [q if q > 1 else 0 for q in pl], self.num_kv_heads,
-                        query.shape[1], kernels.device_cus(query.device))
+                        lens_host, ql, self.num_kv_heads, query.shape[1],
+                        kernels.device_cus(query.device), head_size=self.head_size)
+                    longest = max((l for l, q in zip(lens_host, ql) if q > 0), default=0)
                 kernels.paged_prefill(query[nd:n], key_cache, value_cache,
                                       attn_metadata.block_table, tok[nd:n], pos[nd:n],
                                       scale=self.scale, layout="vllm", output=output[nd:n],
-                                      split_keys=split,
-                                      max_seq_len=attn_metadata.max_seq_len if split else 0)
+                                      split_keys=split, max_seq_len=longest if split else 0)
 
             if n > nd:
                 tok, pos = kernels.build_token_index(attn_metadata.query_start_loc,

@@ -58,6 +58,8 @@ class EngineMLP:
         self._scratch_streams: set = set()
         self._gu: Optional[torch.Tensor] = None
         self._gu_streams: set = set()
+        # Outgrown scratch buffers, kept alive (see _grow).
+        self._retired: list = []
         self.fused_max_tokens = self.FUSED_MAX_TOKENS
 
     def set_weights(self, gate_proj: Optional[torch.Tensor] = None,
@@ -87,17 +89,23 @@ class EngineMLP:
 
     def _grow(self, name: str, n: int, like: torch.Tensor,
               stream: torch.cuda.Stream) -> torch.Tensor:
-        """A scratch of at least n elements kept in attribute `name`,
-        allocated on the stream that writes and reads it, so that when it is
-        outgrown the old block returns to that stream's pool and is reused
-        only by work ordered after the kernels still using it.  A scratch
-        first made on another stream is marked as used on this one
-        (record_stream) before it can be freed."""
+        """A grow-only scratch of at least n elements kept in attribute
+        `name`, allocated on the stream that writes and reads it.  An outgrown
+        buffer is kept alive, never freed, as kernels._GrowOnlyScratch does: a
+        HIP graph captured while it was current holds its address, and a
+        replay must not write into memory the caching allocator has handed to
+        another tensor.  Sizes grow at least 2x, so the kept buffers sum to
+        less than the current one.  A scratch first made on another stream is
+        marked as used on this one (record_stream)."""
         buf, streams = getattr(self, name), getattr(self, name + "_streams")
         if buf is None or buf.numel() < n or buf.dtype != like.dtype or buf.device != like.device:
-            setattr(self, name, None)
+            size = n
+            if buf is not None:
+                self._retired.append(buf)
+                if buf.dtype == like.dtype and buf.device == like.device:
+                    size = max(n, 2 * buf.numel())
             with torch.cuda.stream(stream):
-                buf = torch.empty(n, dtype=like.dtype, device=like.device)
+                buf = torch.empty(size, dtype=like.dtype, device=like.device)
             setattr(self, name, buf)
             setattr(self, name + "_streams", {stream.cuda_stream})
         elif stream.cuda_stream not in streams:

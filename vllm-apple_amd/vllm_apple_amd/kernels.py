@@ -491,10 +491,16 @@ _prefill_ws = _GrowOnlyScratch()
 _PREFILL_KEY_TILE = 64      # keys per prefill tile (paged_prefill.hip)
 _PREFILL_SPLIT_QUANTUM = 1024  # split sizes in multiples of 16 key tiles
 _prefill_split_cache: dict = {}
+# Largest split-K prefill workspace choose_prefill_split plans for: the
+# partials take num_tokens * H * pieces * (D + 2) * 4 bytes, so a long
+# context beside many short prefill tokens gets fewer, longer pieces (or no
+# split) instead of a large allocation in the middle of serving.
+PREFILL_SPLIT_MAX_WORKSPACE = 256 << 20
 
 
 def choose_prefill_split(ctx_lens_host, query_lens_host, num_kv_heads: int,
-                         num_query_heads: int, num_cus: int) -> int:
+                         num_query_heads: int, num_cus: int, head_size: int = 128,
+                         max_workspace_bytes: int = PREFILL_SPLIT_MAX_WORKSPACE) -> int:
     """Key split for a prefill batch (0: none), from the host lengths.
 
     The prefill kernel gives each workgroup a query tile (32 tokens of 4
@@ -505,10 +511,15 @@ def choose_prefill_split(ctx_lens_host, query_lens_host, num_kv_heads: int,
     per-slot share is total / (2 * CUs).  A split is chosen when the longest
     workgroup exceeds 1.5x that share, with pieces of about half the share
     (rounded up to 1024 keys) so the dispatcher can balance the pieces.
+    The pieces are counted over the longest prefill context (pass that as
+    paged_prefill's max_seq_len), and the partials of all prefill tokens
+    (sum of the query lengths) must fit max_workspace_bytes: otherwise the
+    pieces grow until they do, or the split is dropped.
     Memoised per length tuple (every layer of a step sees the same batch).
     """
     key = (tuple(int(x) for x in ctx_lens_host), tuple(int(x) for x in query_lens_host),
-           int(num_kv_heads), int(num_query_heads), int(num_cus))
+           int(num_kv_heads), int(num_query_heads), int(num_cus), int(head_size),
+           int(max_workspace_bytes))
     hit = _prefill_split_cache.get(key)
     if hit is not None:
         return hit
@@ -531,6 +542,18 @@ def choose_prefill_split(ctx_lens_host, query_lens_host, num_kv_heads: int,
         split = -(-piece // _PREFILL_SPLIT_QUANTUM) * _PREFILL_SPLIT_QUANTUM
         if split >= longest * _PREFILL_KEY_TILE:
             split = 0
+    if split:
+        tokens = sum(max(0, q) for q in key[1])
+        row_bytes = num_query_heads * (head_size + 2) * 4
+        max_pieces = max_workspace_bytes // max(1, tokens * row_bytes)
+        keys = longest * _PREFILL_KEY_TILE
+        if -(-keys // split) > max_pieces:
+            split = 0
+            if max_pieces >= 2:
+                split = -(-keys // max_pieces)
+                split = -(-split // _PREFILL_SPLIT_QUANTUM) * _PREFILL_SPLIT_QUANTUM
+                if split >= keys:
+                    split = 0
     if len(_prefill_split_cache) > 4096:
         _prefill_split_cache.clear()
     _prefill_split_cache[key] = split
