@@ -88,11 +88,24 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
     from vllm_apple_amd import _lib
 
     p = _lib.VaaAttnParams()
-    p.head_size = 80
+    # Head sizes: any multiple of 8 up to 128.
+    for bad in (100, 136, 0):
+        p.head_size = bad
+        st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None,
+                                            None, None, None, None, 0, None)
+        assert st == _lib.VAA_ERR_UNSUPPORTED
+        assert f"head_size={bad}" in _lib.last_error()
+        st = lib.vaa_paged_attention_prefill(ctypes.byref(p), None, None, None, None, None,
+                                             None, None, 0, None)
+        assert st == _lib.VAA_ERR_UNSUPPORTED and f"head_size={bad}" in _lib.last_error()
+    p.head_size, p.block_size = 80, 16
     st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
                                         None, None, None, 0, None)
-    assert st == _lib.VAA_ERR_UNSUPPORTED
-    assert "head_size=80" in _lib.last_error()
+    assert st == _lib.VAA_ERR_INVALID_ARG  # head size accepted; the zeroed heads are not
+    assert "heads" in _lib.last_error()
+    p.head_size, p.block_size = 100, 0
+    st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
+                                        None, None, None, 0, None)
     with pytest.raises(NotImplementedError):
         _lib.check(st, "decode")
     st = lib.vaa_rmsnorm(None, None, None, None, 4, 0, 0, 0, 0, 1e-5, 0, None)

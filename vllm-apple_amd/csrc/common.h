@@ -112,6 +112,11 @@ struct Elem<bf16> {
   }
 };
 
+// Attention head sizes: any multiple of 8 (16-byte rows) up to 128, computed at
+// the next multiple of 32 (the MFMA contraction width) with the tail masked.
+inline bool head_size_ok(int hd) { return hd >= 8 && hd <= 128 && hd % 8 == 0; }
+inline int padded_head(int hd) { return (hd + 31) / 32 * 32; }
+
 // Validates vaa_attn_params.dtype.
 inline bool valid_dtype(int32_t dt) { return dt == VAA_DTYPE_F16 || dt == VAA_DTYPE_BF16; }
 

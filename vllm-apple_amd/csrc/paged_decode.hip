@@ -30,6 +30,14 @@
 //              and invalidate per workgroup on every XCD), which measured 3x
 //              slower than the kernel boundary.
 //
+// Head sizes: the kernels compute at D in {32, 64, 96, 128}; a head size hd
+// below D (any multiple of 8, e.g. 80 or 112, as the reference's generic
+// kernels take any head size up to 128: paged_attention_fused.metal:208-233)
+// runs the next larger D with the tail dims zero: Q and K chunks past hd load
+// as zeros (so they add nothing to Q.K), V chunks past hd are not loaded, and
+// only the first hd dims of a row are written.  Those kernels are the kPad
+// instantiations; the four native sizes compile without the masks.
+//
 // Per 16-token tile a wave does
 //   S^T[16 tok x 16 heads] = K[16 x D] * Q^T[D x 16]   (D/32 x mfma 16x16x32)
 //   P = exp2(S*scale*log2e - m)                         (fp32, heads on lanes)
@@ -92,6 +100,7 @@ struct DecodeArgs {
   float* ws_ml;
   int* ws_hdr;
   float scale_log2;
+  int hd;  // head size (<= D; the kPad kernels mask dims hd .. D-1)
   int num_seqs, max_blocks, block_size, num_kv_heads, num_q_heads, G;
   int Gc, chunks;  // query heads per chunk (<= 16) and chunks per kv head
   int part_tiles, max_parts;
@@ -131,6 +140,7 @@ struct LaneMap {
   uint32_t wlds[Cfg<D>::VLD];  // LDS element offset where V chunk i is stored
   uint32_t trbase;             // V^T transposing read: this lane's 8-byte piece at chunk 0
   int trsw;                    // chunk swizzle of its row
+  uint32_t kval, vval;         // kPad: bit s / i set when K step s / V chunk i is below hd
 };
 
 // Block-table window: lane i of `vals` holds the entry of block blk0 + i, so a
@@ -152,7 +162,7 @@ __device__ __forceinline__ int64_t window_block(const DecodeArgs& a, int vals, i
 // (0.638-0.642 against 0.610-0.612 ms with V alone hinted), while on the
 // decode alone it helps (headline 78.4-78.7 % with V alone, 78.8-79.1 % with
 // both, one box).
-template <int D, bool kStream = true>
+template <int D, bool kStream = true, bool kPad = false>
 __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
                                           int64_t vbase, const LaneMap<D>& m,
                                           int64_t phys, int j, Tile<D>& t) {
@@ -160,11 +170,18 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
   if (phys < 0 || phys >= a.num_blocks) phys = 0;  // masked by the caller
   const f16* kb = a.kc + kbase + phys * a.k_sb + row0 * a.k_st;
   const f16* vb = a.vc + vbase + phys * a.v_sb + row0 * a.v_st;
+  const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int s = 0; s < Cfg<D>::NS; ++s)
+  for (int s = 0; s < Cfg<D>::NS; ++s) {
+    if (kPad && !((m.kval >> s) & 1u)) {
+      t.k[s] = z;
+      continue;
+    }
     t.k[s] = kStream ? ld16_stream(kb + m.koff + 32 * s) : ld16(kb + m.koff + 32 * s);
+  }
 #pragma unroll
-  for (int i = 0; i < Cfg<D>::VLD; ++i) t.v[i] = ld16_stream(vb + m.voff[i]);
+  for (int i = 0; i < Cfg<D>::VLD; ++i)
+    t.v[i] = (!kPad || ((m.vval >> i) & 1u)) ? ld16_stream(vb + m.voff[i]) : z;
 }
 
 // One tile of math.  valid = number of real tokens in the tile (16 for every
@@ -246,7 +263,7 @@ struct RangeOut {
 // sequence's length arrived; a wave whose tiles all lie in those blocks
 // (contexts up to 64 blocks) reads its physical blocks from it, one
 // dependent global round trip fewer.
-template <int D, typename T, int NW = kWaves, bool kStream = true>
+template <int D, typename T, int NW = kWaves, bool kStream = true, bool kPad = false>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int qh0, int nh, int L, bool fused,
                                              bool write_new, int t0, int t1, const RangeOut& ro,
@@ -276,6 +293,15 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     m.voff[i] = row * static_cast<uint32_t>(a.v_st) + ch * 8;
     m.wlds[i] = row * D + ((ch ^ swz<D>(row)) * 8);
   }
+  m.kval = 0;
+  m.vval = 0;
+  if constexpr (kPad) {
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) m.kval |= (32 * s + 8 * g < a.hd ? 1u : 0u) << s;
+#pragma unroll
+    for (int i = 0; i < C::VLD; ++i)
+      m.vval |= (((i * kWave + lane) % C::CH) * 8 < a.hd ? 1u : 0u) << i;
+  }
   {
     // ds_read_b64_tr_b16: in each 16-lane group g, lane 4r + j names the
     // 8-byte piece j (dims 4j .. 4j + 3 of a 16-dim step) of token row
@@ -292,7 +318,9 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     const bool hv = c16 < G;
     const f16* qp = a.q + seq * a.q_st + (qh0 + (hv ? c16 : 0)) * a.q_sh + 8 * g;
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) qb[s] = hv ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < C::NS; ++s)
+      qb[s] = (hv && (!kPad || ((m.kval >> s) & 1u))) ? ld16(qp + 32 * s)
+                                                      : u32x4{0u, 0u, 0u, 0u};
   }
 
   T* vt = reinterpret_cast<T*>(smem) + wave * (kTile * D);
@@ -315,20 +343,20 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     const int jl = ce - 1;
     Tile<D> r0, r1, r2;
     int64_t p0 = window_block(a, vals, blk0, cb);
-    issue_tile<D, kStream>(a, kbase, vbase, m, p0, cb, r0);
+    issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p0, cb, r0);
     int64_t p1 = window_block(a, vals, blk0, min(cb + 1, jl));
-    issue_tile<D, kStream>(a, kbase, vbase, m, p1, min(cb + 1, jl), r1);
+    issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p1, min(cb + 1, jl), r1);
     int64_t p2;
     int j = cb;
     for (; j + 3 <= ce; j += 3) {
       p2 = window_block(a, vals, blk0, min(j + 2, jl));
-      issue_tile<D, kStream>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
+      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
       tile_math<D, T>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
       p0 = window_block(a, vals, blk0, min(j + 3, jl));
-      issue_tile<D, kStream>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
+      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
       tile_math<D, T>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
       p1 = window_block(a, vals, blk0, min(j + 4, jl));
-      issue_tile<D, kStream>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
+      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
       tile_math<D, T>(m, r2, qb, vt, valid_of(p2), g, a.scale_log2, m_run, l_part, acc);
     }
     // Remainder (0..2 tiles): r0 holds tile j, r1 tile j+1.
@@ -366,14 +394,18 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
       const f16* kp = mine ? a.new_k + seq * a.n_st + kvh * a.n_sh + 8 * g
                            : kb + m.koff;
 #pragma unroll
-      for (int s = 0; s < C::NS; ++s) t.k[s] = ld16(kp + 32 * s);
-      if (mine && write_new) {
-#pragma unroll
-        for (int s = 0; s < C::NS; ++s) st16(kb + m.koff + 32 * s, t.k[s]);
+      for (int s = 0; s < C::NS; ++s) {
+        const bool in = !kPad || ((m.kval >> s) & 1u);
+        t.k[s] = in ? ld16(kp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+        if (in && mine && write_new) st16(kb + m.koff + 32 * s, t.k[s]);
       }
     }
 #pragma unroll
     for (int i = 0; i < C::VLD; ++i) {
+      if (kPad && !((m.vval >> i) & 1u)) {
+        t.v[i] = u32x4{0u, 0u, 0u, 0u};
+        continue;
+      }
       const bool mine = (m.vrow[i] == new_row) && bvalid;
       const int ch = (i * kWave + lane) % C::CH;
       const f16* vp = mine ? a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8 : vb + m.voff[i];
@@ -426,8 +458,9 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
     }
     if (ro.whole) {
       const int qh = qh0 + h;
-      reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
-          Elem<T>::from_f(den > 0.f ? num / den : 0.f);
+      if (!kPad || d < a.hd)
+        reinterpret_cast<T*>(a.out)[seq * a.o_st + qh * a.o_sh + d] =
+            Elem<T>::from_f(den > 0.f ? num / den : 0.f);
     } else {
       const int64_t row = ro.prow0 + h * ro.prow_step;
       a.ws_acc[row * D + d] = num;
@@ -462,7 +495,7 @@ __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int seq) {
 // fastest).  NW waves per workgroup: 8 for long partitions; 4 for short
 // ones, so that two workgroups share a CU and one's start-up (Q load, first
 // tiles) overlaps the other's tail.
-template <int D, typename T, int NW>
+template <int D, typename T, int NW, bool kPad>
 __global__ void __launch_bounds__(NW* kWave)
 paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -475,7 +508,7 @@ paged_decode_kernel(DecodeArgs a) {
   const int Lorig = a.seq_lens[seq];
   const int L = clamped_len(a, seq);
   if (L <= 0) {
-    if (part == 0) zero_rows(a, seq, qh0, nh, D);
+    if (part == 0) zero_rows(a, seq, qh0, nh, a.hd);
     return;
   }
   const int part_tok = a.part_tiles * kTile;
@@ -488,7 +521,7 @@ paged_decode_kernel(DecodeArgs a) {
   ro.whole = (n_parts == 1);
   ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh0) * a.max_parts + part;
   ro.prow_step = a.max_parts;
-  decode_range<D, T, NW>(a, smem, seq, kvh, qh0, nh, L,
+  decode_range<D, T, NW, true, kPad>(a, smem, seq, kvh, qh0, nh, L,
                          a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro, false, part == 0,
                          pre);
 }
@@ -537,7 +570,7 @@ __device__ __forceinline__ void tile_prefix(const DecodeArgs& a, int* starts, in
   __syncthreads();
 }
 
-template <int D, typename T, int NW>
+template <int D, typename T, int NW, bool kPad>
 __global__ void __launch_bounds__(NW* kWave)
 paged_decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -573,7 +606,7 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(y) * (nc + B) + c + seq) * a.Gc;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T, NW, NW != kSharedWaves>(a, smem, seq, kvh, qh0, nh, L,
+    decode_range<D, T, NW, NW != kSharedWaves, kPad>(a, smem, seq, kvh, qh0, nh, L,
                            a.new_k != nullptr && a.seq_lens[seq] == L, hc == 0, t0, t1, ro,
                            true);
     pos = s0 + t1;
@@ -633,6 +666,7 @@ paged_decode_merge_balanced_kernel(DecodeArgs a) {
   const int d4 = threadIdx.x % D4;
   if (qh >= a.num_q_heads) return;
   const int B = a.num_seqs, nc = a.max_parts;
+  if (4 * d4 >= a.hd) return;  // padded dims (hd is a multiple of 8)
   T* o = reinterpret_cast<T*>(a.out) + seq * a.o_st + qh * a.o_sh + 4 * d4;
   const int L = clamped_len(a, seq);
   if (L <= 0) {
@@ -690,7 +724,7 @@ paged_decode_merge_kernel(DecodeArgs a) {
   }
   snum[grp][d4] = m.num;
   __syncthreads();
-  if (grp != 0) return;
+  if (grp != 0 || 4 * d4 >= a.hd) return;
   MergeAcc4 t;
 #pragma unroll
   for (int g = 0; g < kMergeSplit; ++g) t.add(sml[g][0], sml[g][1], snum[g][d4]);
@@ -794,7 +828,7 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
   if (max_len < 1) max_len = 1;
   const int quantum = kTile * kWaves;
   int64_t part = p->partition_size;
-  const size_t row_bytes = (static_cast<size_t>(p->head_size) + 2) * sizeof(float);
+  const size_t row_bytes = (static_cast<size_t>(padded_head(p->head_size)) + 2) * sizeof(float);
   if (part == VAA_PARTITION_BALANCED || part == VAA_PARTITION_BALANCED_SHARED) {
     if (p->num_seqs > kBalMaxSeqs)
       return fail(VAA_ERR_UNSUPPORTED, "balanced split: num_seqs=%d > %d", p->num_seqs,
@@ -848,10 +882,9 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
 
 int check_params(const vaa_attn_params* p, const char* what) {
   if (!p) return fail(VAA_ERR_INVALID_ARG, "%s: null params", what);
-  if (p->head_size != 32 && p->head_size != 64 && p->head_size != 96 &&
-      p->head_size != 128)
-    return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d not in {32,64,96,128}",
-                what, p->head_size);
+  if (!head_size_ok(p->head_size))
+    return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d (a multiple of 8 up to 128)", what,
+                p->head_size);
   if (p->block_size <= 0 || p->block_size % kTile != 0)
     return fail(VAA_ERR_UNSUPPORTED, "%s: block_size=%d must be a multiple of 16",
                 what, p->block_size);
@@ -882,7 +915,7 @@ int check_params(const vaa_attn_params* p, const char* what) {
   return VAA_OK;
 }
 
-template <int D, typename T>
+template <int D, typename T, bool kPad>
 int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t stream) {
   DecodeArgs a = a0;
   const size_t lds_tiles = static_cast<size_t>(kWaves) * kTile * D * sizeof(f16);
@@ -897,12 +930,12 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
     a.lds_main = static_cast<int>((lds_bal + 15) / 16 * 16);
     const size_t lds_b = a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kWaves) * sizeof(int);
     if (shared)
-      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kSharedWaves>),
+      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kSharedWaves, kPad>),
                          dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kSharedWaves * kWave),
                          lds_b,
                          stream, a);
     else
-      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kWaves>),
+      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kWaves, kPad>),
                          dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kWaves * kWave), lds_b,
                          stream, a);
     int st = check_launch("paged_decode_balanced_kernel");
@@ -918,11 +951,11 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
     const size_t lds4 = std::max(static_cast<size_t>(kNw) * kTile * D * sizeof(f16),
                                  (2 * kNw * 16 + static_cast<size_t>(kNw) * a.Gc * D) *
                                      sizeof(float));
-    hipLaunchKernelGGL((paged_decode_kernel<D, T, kNw>), grid, dim3(kNw * kWave), lds4, stream,
-                       a);
-  } else {
-    hipLaunchKernelGGL((paged_decode_kernel<D, T, kWaves>), grid, dim3(kWaves * kWave), lds,
+    hipLaunchKernelGGL((paged_decode_kernel<D, T, kNw, kPad>), grid, dim3(kNw * kWave), lds4,
                        stream, a);
+  } else {
+    hipLaunchKernelGGL((paged_decode_kernel<D, T, kWaves, kPad>), grid, dim3(kWaves * kWave),
+                       lds, stream, a);
   }
   int st = check_launch("paged_decode_kernel");
   if (st || a.max_parts <= 1) return st;
@@ -996,13 +1029,15 @@ int decode_impl(const char* what, const vaa_attn_params* p, const uint16_t* quer
     if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
       return fail(VAA_ERR_INVALID_ARG,
                   "%s: workspace must be 16-byte aligned", what);
-    const size_t rows = (sp.ws_bytes - sp.hdr_bytes) / ((p->head_size + 2) * sizeof(float));
+    const int dp = padded_head(p->head_size);
+    const size_t rows = (sp.ws_bytes - sp.hdr_bytes) / ((dp + 2) * sizeof(float));
     unsigned char* base = static_cast<unsigned char*>(workspace);
     a.ws_hdr = reinterpret_cast<int*>(base);
     a.ws_acc = reinterpret_cast<float*>(base + sp.hdr_bytes);
-    a.ws_ml = a.ws_acc + rows * p->head_size;
+    a.ws_ml = a.ws_acc + rows * dp;
   }
   a.scale_log2 = p->scale * kLog2e;
+  a.hd = p->head_size;
   a.num_seqs = p->num_seqs;
   a.max_blocks = p->max_blocks_per_seq;
   a.block_size = p->block_size;
@@ -1023,16 +1058,21 @@ int decode_impl(const char* what, const vaa_attn_params* p, const uint16_t* quer
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = p->dtype == VAA_DTYPE_BF16;
-  switch (p->head_size) {
-    case 32: return bf ? launch_decode<32, bf16>(a, sp.balanced, sp.shared, s)
-                       : launch_decode<32, f16>(a, sp.balanced, sp.shared, s);
-    case 64: return bf ? launch_decode<64, bf16>(a, sp.balanced, sp.shared, s)
-                       : launch_decode<64, f16>(a, sp.balanced, sp.shared, s);
-    case 96: return bf ? launch_decode<96, bf16>(a, sp.balanced, sp.shared, s)
-                       : launch_decode<96, f16>(a, sp.balanced, sp.shared, s);
-    case 128: return bf ? launch_decode<128, bf16>(a, sp.balanced, sp.shared, s)
-                        : launch_decode<128, f16>(a, sp.balanced, sp.shared, s);
+  const bool pad = padded_head(p->head_size) != p->head_size;
+#define VAA_DECODE_CASE(DP)                                                              \
+  case DP:                                                                               \
+    if (pad)                                                                             \
+      return bf ? launch_decode<DP, bf16, true>(a, sp.balanced, sp.shared, s)            \
+                : launch_decode<DP, f16, true>(a, sp.balanced, sp.shared, s);            \
+    return bf ? launch_decode<DP, bf16, false>(a, sp.balanced, sp.shared, s)             \
+              : launch_decode<DP, f16, false>(a, sp.balanced, sp.shared, s);
+  switch (padded_head(p->head_size)) {
+    VAA_DECODE_CASE(32)
+    VAA_DECODE_CASE(64)
+    VAA_DECODE_CASE(96)
+    VAA_DECODE_CASE(128)
   }
+#undef VAA_DECODE_CASE
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
 }
 

@@ -34,6 +34,11 @@
 // pieces of row r and lane i receives element i of rows 0..3) hit distinct
 // banks.  V rows past the context or in a missing block are zero-filled, so
 // masked keys (P = 0) contribute exactly zero.
+//
+// Head sizes: the kernel computes at D in {32, 64, 96, 128}; a head size hd
+// below D (a multiple of 8) runs the next larger D with the chunks past hd
+// zero-filled in LDS instead of loaded, Q's past hd zero, and only the first
+// hd dims of a row written (the kPad instantiations).
 #include "common.h"
 
 namespace vaa {
@@ -59,6 +64,7 @@ struct PrefillArgs {
   const int32_t* pos;
   f16* out;
   float scale_log2;
+  int hd;                     // head size (<= D; the kPad kernels mask dims hd .. D-1)
   int num_tokens, num_seqs, max_blocks, block_size, G;
   int bs_shift;               // log2(block_size) when it is a power of two, else -1
   int heads_per_wg, subtiles, head_chunks;
@@ -190,6 +196,7 @@ struct Lanes {
   int row[PCfg<D>::NI];        // row inside the 16-key group for each direct load
   int kaddr[PCfg<D>::NK];      // LDS byte address of the K operand for step s
   int vaddr[PCfg<D>::NDT];     // LDS byte address of the V^T operand for dim tile dt
+  uint32_t kval, vval;         // bit q: direct load q's K / V chunk lies below hd
 };
 
 template <int D>
@@ -205,6 +212,15 @@ __device__ __forceinline__ void lanes_init(const PrefillArgs& a, int wave, int l
     L.row[q] = R & 15;
     L.koff[q] = static_cast<uint32_t>((R & 15) * a.k_st * 2 + lck * 16);
     L.voff[q] = static_cast<uint32_t>((R & 15) * a.v_st * 2 + lcv * 16);
+  }
+  L.kval = 0;
+  L.vval = 0;
+#pragma unroll
+  for (int q = 0; q < C::NI; ++q) {
+    const int P = 64 * (wave * C::NI + q) + lane;
+    const int R = P / C::CH;
+    L.kval |= (((P % C::CH) ^ swzk<D>(R)) * 8 < a.hd ? 1u : 0u) << q;
+    L.vval |= (((P % C::CH) ^ swz<D>(R)) * 8 < a.hd ? 1u : 0u) << q;
   }
   const int qj = lane & 31, hb = lane >> 5;
   const int sk = swzk<D>(qj);
@@ -246,7 +262,7 @@ __device__ __forceinline__ int row_splits(const PrefillArgs& a, int pos) {
 // Streams one 64-key tile into (kd, vd): wave w copies 16-key group w with
 // direct loads, or zeros for rows past the context and for a missing block.
 // kbase / vbase point at this kv head's slice of block 0.
-template <int D>
+template <int D, bool kPad>
 __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* bts,
                                            const char* kbase, const char* vbase, int key0,
                                            int kv_len, int wave, int lane, const Lanes<D>& L,
@@ -270,21 +286,31 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
   if (nvalid > 0) {
     const char* kb = kbase + 2 * (mine * a.k_sb + static_cast<int64_t>(row0) * a.k_st);
     const char* vb = vbase + 2 * (mine * a.v_sb + static_cast<int64_t>(row0) * a.v_st);
+    const u32x4 z = {0u, 0u, 0u, 0u};
     if (nvalid == 16) {  // every tile but a sequence's last
 #pragma unroll
       for (int q = 0; q < C::NI; ++q) {
-        dma16(kb + L.koff[q], kl0 + 1024 * q);
-        dma16(vb + L.voff[q], vl0 + 1024 * q);
+        if constexpr (kPad) {
+          // Chunks past hd: zeros instead of the next row's elements.
+          if ((L.kval >> q) & 1u) dma16(kb + L.koff[q], kl0 + 1024 * q);
+          else *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
+          if ((L.vval >> q) & 1u) dma16(vb + L.voff[q], vl0 + 1024 * q);
+          else *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
+        } else {
+          dma16(kb + L.koff[q], kl0 + 1024 * q);
+          dma16(vb + L.voff[q], vl0 + 1024 * q);
+        }
       }
       return;
     }
 #pragma unroll
     for (int q = 0; q < C::NI; ++q) {
       if (L.row[q] < nvalid) {
-        dma16(kb + L.koff[q], kl0 + 1024 * q);
-        dma16(vb + L.voff[q], vl0 + 1024 * q);
+        if (!kPad || ((L.kval >> q) & 1u)) dma16(kb + L.koff[q], kl0 + 1024 * q);
+        else *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
+        if (!kPad || ((L.vval >> q) & 1u)) dma16(vb + L.voff[q], vl0 + 1024 * q);
+        else *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
       } else {
-        const u32x4 z = {0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
         *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
       }
@@ -409,7 +435,7 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
   }
 }
 
-template <int D, typename T>
+template <int D, typename T, bool kPad>
 __global__ void __launch_bounds__(kThreadsP) __attribute__((amdgpu_waves_per_eu(2, 2)))
 paged_prefill_kernel(PrefillArgs a) {
   using C = PCfg<D>;
@@ -471,7 +497,9 @@ paged_prefill_kernel(PrefillArgs a) {
     const f16* qp = a.q + static_cast<int64_t>(ld ? tok : 0) * a.q_st + head * a.q_sh +
                     hb * (D / 2);
 #pragma unroll
-    for (int s = 0; s < C::NK; ++s) qb[s] = ld ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < C::NK; ++s)
+      qb[s] = (ld && (!kPad || hb * (D / 2) + 8 * s < a.hd)) ? ld16(qp + 8 * s)
+                                                             : u32x4{0u, 0u, 0u, 0u};
   }
 
   float m_run = -INFINITY, l_part = 0.f;
@@ -519,19 +547,19 @@ paged_prefill_kernel(PrefillArgs a) {
       BlockWindow win;
       window_load(a, bts, a.bs_shift >= 0 ? (t_lo * kKT) >> a.bs_shift
                                           : (t_lo * kKT) / a.block_size, win);
-      tile_fetch<D>(a, bts, kbase, vbase, t_lo * kKT, kv_len, wave, lane, L, win, k0s, v0s);
+      tile_fetch<D, kPad>(a, bts, kbase, vbase, t_lo * kKT, kv_len, wave, lane, L, win, k0s, v0s);
       wait_all();
       __builtin_amdgcn_s_barrier();
       for (int kt = t_lo; kt < t_hi; kt += 2) {
         if (kt + 1 < t_hi)
-          tile_fetch<D>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
+          tile_fetch<D, kPad>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
                         v1s);
         if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
         wait_all();
         __builtin_amdgcn_s_barrier();
         if (kt + 1 >= t_hi) break;
         if (kt + 2 < t_hi)
-          tile_fetch<D>(a, bts, kbase, vbase, (kt + 2) * kKT, kv_len, wave, lane, L, win, k0s,
+          tile_fetch<D, kPad>(a, bts, kbase, vbase, (kt + 2) * kKT, kv_len, wave, lane, L, win, k0s,
                         v0s);
         if (math)
           tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
@@ -582,7 +610,7 @@ paged_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = Elem<T>::from_f(acc[dt][4 * rg + i] * inv);
       const int d = 32 * dt + 8 * rg + 4 * hb;
-      *reinterpret_cast<typename Elem<T>::x4*>(op + d) = o;
+      if (!kPad || d < a.hd) *reinterpret_cast<typename Elem<T>::x4*>(op + d) = o;
     }
   }
 }
@@ -645,6 +673,7 @@ __global__ void __launch_bounds__(kMergeThreads) prefill_merge_kernel(PrefillArg
       const int it = it0 + i * kMergeThreads;
       if (it >= H * G4 || aborted[i]) continue;
       const int head = it / G4, d = (it % G4) * 4;
+      if (d >= a.hd) continue;  // padded dims (hd is a multiple of 8)
       T* o = reinterpret_cast<T*>(a.out) + static_cast<int64_t>(tok) * a.o_st + head * a.o_sh + d;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -653,7 +682,7 @@ __global__ void __launch_bounds__(kMergeThreads) prefill_merge_kernel(PrefillArg
   }
 }
 
-template <int D, typename T>
+template <int D, typename T, bool kPad>
 int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   const int per_wg = kQT * a.subtiles;
   const int gx = (a.num_tokens + per_wg - 1) / per_wg, gy = num_kv_heads * a.head_chunks;
@@ -664,7 +693,7 @@ int launch_prefill(const PrefillArgs& a, int num_kv_heads, hipStream_t stream) {
   b.tiles_y = gy;
   b.padded_tiles = padded;
   dim3 grid(gx, (padded + gx - 1) / gx, a.split_tiles > 0 ? a.n_splits : 1);
-  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), grid, dim3(kThreadsP), 0, stream, b);
+  hipLaunchKernelGGL((paged_prefill_kernel<D, T, kPad>), grid, dim3(kThreadsP), 0, stream, b);
   const int st = check_launch("paged_prefill_kernel");
   if (st || a.split_tiles <= 0) return st;
   hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(a.num_tokens), dim3(kMergeThreads), 0,
@@ -703,7 +732,7 @@ int prefill_split_plan(const char* what, const vaa_attn_params* p, int split_key
 size_t prefill_ws_bytes(const vaa_attn_params* p, int num_tokens, int n_splits) {
   if (n_splits <= 1 || num_tokens <= 0) return 0;
   return static_cast<size_t>(num_tokens) * p->num_query_heads * n_splits *
-         (static_cast<size_t>(p->head_size) + 2) * sizeof(float);
+         (static_cast<size_t>(padded_head(p->head_size)) + 2) * sizeof(float);
 }
 
 int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* query,
@@ -712,9 +741,8 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
                  const int32_t* positions, uint16_t* output, int num_tokens, int split_keys,
                  void* workspace, size_t workspace_bytes, void* stream) {
   if (!p) return fail(VAA_ERR_INVALID_ARG, "%s: null params", what);
-  if (p->head_size != 32 && p->head_size != 64 && p->head_size != 96 &&
-      p->head_size != 128)
-    return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d not in {32,64,96,128}", what,
+  if (!head_size_ok(p->head_size))
+    return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d (a multiple of 8 up to 128)", what,
                 p->head_size);
   if (p->block_size <= 0 || p->num_kv_heads <= 0 || p->num_query_heads <= 0 ||
       p->num_query_heads % p->num_kv_heads != 0 ||
@@ -764,7 +792,7 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
       return fail(VAA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", what);
     const size_t rows = static_cast<size_t>(num_tokens) * p->num_query_heads * n_splits;
     a.ws_acc = static_cast<float*>(workspace);
-    a.ws_ml = a.ws_acc + rows * p->head_size;
+    a.ws_ml = a.ws_acc + rows * padded_head(p->head_size);
   }
   a.q = reinterpret_cast<const f16*>(query);
   a.kc = reinterpret_cast<const f16*>(key_cache);
@@ -774,6 +802,7 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
   a.pos = positions;
   a.out = reinterpret_cast<f16*>(output);
   a.scale_log2 = p->scale * kLog2e;
+  a.hd = p->head_size;
   a.num_tokens = num_tokens;
   a.num_seqs = p->num_seqs;
   a.max_blocks = p->max_blocks_per_seq;
@@ -799,16 +828,21 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
   a.o_st = p->o_stride_token; a.o_sh = p->o_stride_head;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = p->dtype == VAA_DTYPE_BF16;
-  switch (p->head_size) {
-    case 32: return bf ? launch_prefill<32, bf16>(a, p->num_kv_heads, s)
-                       : launch_prefill<32, f16>(a, p->num_kv_heads, s);
-    case 64: return bf ? launch_prefill<64, bf16>(a, p->num_kv_heads, s)
-                       : launch_prefill<64, f16>(a, p->num_kv_heads, s);
-    case 96: return bf ? launch_prefill<96, bf16>(a, p->num_kv_heads, s)
-                       : launch_prefill<96, f16>(a, p->num_kv_heads, s);
-    case 128: return bf ? launch_prefill<128, bf16>(a, p->num_kv_heads, s)
-                        : launch_prefill<128, f16>(a, p->num_kv_heads, s);
+  const bool pad = padded_head(p->head_size) != p->head_size;
+#define VAA_PREFILL_CASE(DP)                                                 \
+  case DP:                                                                   \
+    if (pad)                                                                 \
+      return bf ? launch_prefill<DP, bf16, true>(a, p->num_kv_heads, s)      \
+                : launch_prefill<DP, f16, true>(a, p->num_kv_heads, s);      \
+    return bf ? launch_prefill<DP, bf16, false>(a, p->num_kv_heads, s)       \
+              : launch_prefill<DP, f16, false>(a, p->num_kv_heads, s);
+  switch (padded_head(p->head_size)) {
+    VAA_PREFILL_CASE(32)
+    VAA_PREFILL_CASE(64)
+    VAA_PREFILL_CASE(96)
+    VAA_PREFILL_CASE(128)
   }
+#undef VAA_PREFILL_CASE
   return fail(VAA_ERR_UNSUPPORTED, "head_size=%d", p->head_size);
 }
 

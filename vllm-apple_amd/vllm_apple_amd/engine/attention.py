@@ -98,8 +98,11 @@ class PagedAttentionOp:
 
     def __init__(self, context: Any, num_kv_heads: int, num_query_heads: int, head_size: int,
                  block_size: int, scale: Optional[float] = None):
-        if head_size not in (32, 64, 96, 128):
-            raise ValueError(f"head_size must be 32/64/96/128, got {head_size}")
+        # The reference's h128 kernel takes 128 and its generic kernels any
+        # head size up to 128 (engine/ops/attention.py:268-290); the HIP
+        # kernels take any multiple of 8 up to 128 (16-byte rows).
+        if not (8 <= head_size <= 128 and head_size % 8 == 0):
+            raise ValueError(f"head_size must be a multiple of 8 up to 128, got {head_size}")
         if num_query_heads % num_kv_heads != 0:
             raise ValueError("num_query_heads must be a multiple of num_kv_heads")
         self._context = context

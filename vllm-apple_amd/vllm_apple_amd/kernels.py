@@ -544,7 +544,8 @@ def choose_prefill_split(ctx_lens_host, query_lens_host, num_kv_heads: int,
             split = 0
     if split:
         tokens = sum(max(0, q) for q in key[1])
-        row_bytes = num_query_heads * (head_size + 2) * 4
+        # Partial rows are computed at the head size rounded up to 32.
+        row_bytes = num_query_heads * (-(-head_size // 32) * 32 + 2) * 4
         max_pieces = max_workspace_bytes // max(1, tokens * row_bytes)
         keys = longest * _PREFILL_KEY_TILE
         if -(-keys // split) > max_pieces:
