@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, host
+from helpers import assert_close, host, assert_close_bf16
 
 import oracle.layer_ops as olo
 
@@ -43,9 +43,8 @@ def test_gate_up_silu_vs_oracle(gpu, T, H, I, dtype):
     ref = olo.gate_up_silu(x.double().numpy(), w.double().numpy())
     if dtype == torch.float16:
         assert_close(host(out), ref, what=f"gate_up_silu {T}x{H}x{I}")
-    else:  # bf16 outputs: the same bound with bf16's 8 significand bits
-        assert_close(out.cpu().double().numpy(), ref, atol=8 * 2e-3, rtol=1e-2,
-                     what=f"gate_up_silu bf16 {T}x{H}x{I}")
+    else:  # bf16 outputs: the same bound plus the bf16 output rounding
+        assert_close_bf16(out.cpu().double().numpy(), ref, what=f"gate_up_silu bf16 {T}x{H}x{I}")
 
 
 def test_gate_up_silu_vs_unfused_reference_order(gpu):

@@ -175,9 +175,11 @@ def test_kv_write_slots_padded_head_sizes(gpu, D):
     vc = torch.randn(nb, KV, bs, D, generator=g).half()
     k = torch.randn(T, KV, D, generator=g).half()
     v = torch.randn(T, KV, D, generator=g).half()
-    slots = torch.randperm(nb * bs, generator=g)[:T].to(torch.int64)
-    slots[::7] = -1
-    slots[0] = nb * bs - 1  # the pool's last row
+    perm = torch.randperm(nb * bs, generator=g).to(torch.int64)
+    last = int((perm == nb * bs - 1).nonzero()[0])
+    perm[0], perm[last] = nb * bs - 1, perm[0].item()  # the pool's last row, once
+    slots = perm[:T].clone()
+    slots[1::7] = -1
     kb, kd = _canaried(kc)
     vb, vd = _canaried(vc)
     kernels.kv_write_slots(k.cuda(), v.cuda(), kd, vd, slots.cuda())

@@ -77,6 +77,9 @@ template <>
 struct Elem<f16> {
   using x4 = f16x4;
   using x8 = f16x8;
+  // Probabilities enter the PV product as one fp16 value (11 significant
+  // bits).
+  static constexpr bool kSplitP = false;
   static __device__ __forceinline__ float to_f(f16 v) { return static_cast<float>(v); }
   static __device__ __forceinline__ f16 from_f(float v) { return static_cast<f16>(v); }
   // D[16x16] += A[16x32] B[32x16]
@@ -97,6 +100,12 @@ template <>
 struct Elem<bf16> {
   using x4 = bf16x4;
   using x8 = bf16x8;
+  // Probabilities enter the PV product as a bf16 pair p = hi + lo (16
+  // significant bits) and two MFMAs: one bf16 value (8 bits) puts an error
+  // of 2^-9 p_k |v_k| on every term, which on short contexts with values of
+  // opposite sign reaches the attention tolerance (measured on MI355X: up to
+  // 0.93 of |d| <= 2e-3 + 1e-2 |ref| in decode, 10x the fp16 path's error).
+  static constexpr bool kSplitP = true;
   static __device__ __forceinline__ float to_f(bf16 v) { return static_cast<float>(v); }
   // Round to nearest even (v_cvt_pk_bf16_f32).
   static __device__ __forceinline__ bf16 from_f(float v) { return static_cast<bf16>(v); }

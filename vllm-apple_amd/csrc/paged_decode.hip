@@ -225,11 +225,19 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
     m_run = m_new;
   }
   const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
-  typename Elem<T>::x4 ph;
+  // The sum takes the probabilities as the PV product sees them: the rounded
+  // fp16 value, or the bf16 pair hi + lo (Elem<T>::kSplitP).
+  typename Elem<T>::x4 ph, pl;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    ph[r] = Elem<T>::from_f(fast_exp2(x[r] - m_sub));
-    l_part += Elem<T>::to_f(ph[r]);
+    const float p = fast_exp2(x[r] - m_sub);
+    ph[r] = Elem<T>::from_f(p);
+    if constexpr (Elem<T>::kSplitP) {
+      pl[r] = Elem<T>::from_f(p - Elem<T>::to_f(ph[r]));
+      l_part += Elem<T>::to_f(ph[r]) + Elem<T>::to_f(pl[r]);
+    } else {
+      l_part += Elem<T>::to_f(ph[r]);
+    }
   }
   // O^T += V^T P^T; lane receives V[4g+r][16dt + c16], r = 0..3, from one
   // transposing LDS read (four 16-bit reads before: headline 81.0-81.2 ->
@@ -241,6 +249,7 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
         __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) i16x4*)(vt + m.trbase + (((2 * dt) ^ m.trsw) << 3))));
     acc[dt] = Elem<T>::mfma16x16x16(va, ph, acc[dt]);
+    if constexpr (Elem<T>::kSplitP) acc[dt] = Elem<T>::mfma16x16x16(va, pl, acc[dt]);
   }
 }
 

@@ -412,14 +412,18 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
     m_run = mx;
   }
   const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
-  // pb[g]: B operand for 16-key group g (keys 16g + 8(i/4) + 4hb + i%4).
-  X8 pb[4];
+  // pb[g]: B operand for 16-key group g (keys 16g + 8(i/4) + 4hb + i%4);
+  // with Elem<T>::kSplitP (bf16) p = pb + pl, two PV products.
+  X8 pb[4], pl[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float p = fast_exp2(fmaf(sacc[j][r], a.scale_log2, -m_sub));
       pb[2 * j + (r >> 3)][r & 7] = Elem<T>::from_f(p);
+      if constexpr (Elem<T>::kSplitP)
+        pl[2 * j + (r >> 3)][r & 7] =
+            Elem<T>::from_f(p - Elem<T>::to_f(pb[2 * j + (r >> 3)][r & 7]));
       l_part += p;
     }
   __builtin_amdgcn_sched_barrier(0);
@@ -431,6 +435,7 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
     const X8 va = {vlo[i][0], vlo[i][1], vlo[i][2], vlo[i][3],
                    vhi[i][0], vhi[i][1], vhi[i][2], vhi[i][3]};
     acc[dt] = Elem<T>::mfma32x32x16(va, pb[g], acc[dt]);
+    if constexpr (Elem<T>::kSplitP) acc[dt] = Elem<T>::mfma32x32x16(va, pl[g], acc[dt]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
