@@ -139,6 +139,39 @@ def test_prefill_bf16(gpu, D, H, KV):
     assert_close_bf16(vals(out), ref, what=f"bf16 prefill D={D}")
 
 
+def test_bf16_short_contexts(gpu):
+    """Few keys with values of opposite sign: the case where one bf16
+    probability per key (8 bits) reached the attention bound (up to 1.03 of
+    it on 5 keys).  Decode (every split mode) and prefill with no prefix."""
+    from vllm_apple_amd import kernels
+
+    lens = [2, 3, 5, 9, 17, 40, 90, 200]
+    kc, vc, bt, g = _paged(len(lens), 32, 8, 128, lens, seed=6)
+    q = torch.randn(len(lens), 32, 128, generator=g).bfloat16()
+    L = torch.tensor(lens, dtype=torch.int32)
+    ref = oat.decode(vals(q), vals(kc), vals(vc), bt.numpy(), L.numpy(), 1 / math.sqrt(128))
+    for part in (0, 128, -1, -2):
+        out = kernels.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), L.cuda(),
+                                   scale=1 / math.sqrt(128), max_seq_len=max(lens),
+                                   partition_size=part)
+        torch.cuda.synchronize()
+        assert_close_bf16(vals(out), ref, what=f"bf16 short decode part={part}")
+    ctx = [5, 9, 40]
+    kc, vc, bt, g = _paged(3, 32, 8, 128, ctx, seed=7)
+    tok = sum(([s] * n for s, n in enumerate(ctx)), [])
+    pos = sum((list(range(n)) for n in ctx), [])
+    q = torch.randn(len(tok), 32, 128, generator=g).bfloat16()
+    tok_t = torch.tensor(tok, dtype=torch.int32)
+    pos_t = torch.tensor(pos, dtype=torch.int32)
+    out = kernels.paged_prefill(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), tok_t.cuda(),
+                                pos_t.cuda(), scale=1 / math.sqrt(128))
+    torch.cuda.synchronize()
+    ref, written = oat.prefill(vals(q), vals(kc), vals(vc), bt.numpy(), tok_t.numpy(),
+                               pos_t.numpy(), 1 / math.sqrt(128))
+    assert written.all()
+    assert_close_bf16(vals(out), ref, what="bf16 short prefill")
+
+
 def test_mixed_dtypes_are_rejected(gpu):
     from vllm_apple_amd import kernels
 
