@@ -15,7 +15,9 @@
 //   For each distinct sequence among the tile's tokens (normally one) the
 //   workgroup walks 64-key tiles of that sequence's cache:
 //     S^T[64 keys x 32 queries] = K Q^T   (2 x D/16 mfma 32x32x16)
-//     P = exp2(S*scale*log2e - m), causal/row mask as -inf
+//     P = exp2(S*scale*log2e - m), causal/row mask as -inf (fp16: Q is
+//       prescaled by scale*log2e and the accumulators start at -m, so the
+//       MFMAs deliver the exponent directly)
 //     O^T[D x 32 queries]      += V^T P^T (D/32 x 4 mfma 32x32x16)
 //   The MFMA output layout of S^T (lane = query, 16 keys per lane) is the B
 //   operand layout of the PV product, so the per-query softmax statistics sit
@@ -328,21 +330,24 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
 // One 64-key tile for this wave's 32 query rows: S^T = K Q^T as two
 // independent 32-key MFMA row blocks, online softmax over both, then
 // O^T += V^T P^T over four 16-key groups.  The LDS operand reads run ahead
-// of their MFMAs (kKAhead K reads, kVAhead V^T pairs; the first V^T pairs are
-// issued before the softmax, whose VALU work then hides their latency), and
-// scheduling barriers keep the compiler from hoisting every read (which
+// of their MFMAs (kKAhead K reads, kVAhead V^T pairs; the first V^T pairs
+// are issued before the softmax, whose VALU work then hides their latency),
+// and scheduling barriers keep the compiler from hoisting every read (which
 // would not fit the register budget of two waves per SIMD).  With the direct
 // loads untracked (dma16) the compiler waits for each read with a partial
-// lgkmcnt, so four reads ahead hide as much as six (C3 89.3-89.9 against
-// 89.8-90.2 us) in fewer registers (245 VGPRs at D = 128).
-constexpr int kKAhead = 4;
+// lgkmcnt, so a few reads ahead suffice.  fp16 at D = 128 reads three K
+// operands ahead: its accumulator-initialisation tile (minit) takes the
+// registers of the fourth (256 VGPRs, no spills); the rest keep four.
+template <int D, typename T>
+constexpr int kKAhead = (D == 128 && !Elem<T>::kSplitP) ? 3 : 4;
 constexpr int kVAhead = 4;
 
 template <int D, typename T>
 __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, const f16* vt,
                                           int key0, int lim, int hb, const Lanes<D>& L,
                                           const u32x4 (&qb)[PCfg<D>::NK], float& m_run,
-                                          float& l_part, f32x16 (&acc)[PCfg<D>::NDT]) {
+                                          float& l_part, f32x16 (&acc)[PCfg<D>::NDT],
+                                          f32x16& minit) {
   using C = PCfg<D>;
   using X4 = typename Elem<T>::x4;
   using X8 = typename Elem<T>::x8;
@@ -357,16 +362,24 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
     kA[i] = *reinterpret_cast<const u32x4*>(kbytes + L.kaddr[i >> 1] + 32 * (i & 1) * C::ROWB);
   };
 #pragma unroll
-  for (int i = 0; i < kKAhead && i < NKR; ++i) kread(i);
+  for (int i = 0; i < kKAhead<D, T> && i < NKR; ++i) kread(i);
   __builtin_amdgcn_sched_barrier(0);
+  // fp16: Q is prescaled by scale*log2(e) and both accumulator chains start
+  // at -m_sub (minit), so S^T comes out of the MFMAs as s - m_sub in the
+  // log2 domain and p = 2^(that) is one v_exp_f32.
   f32x16 sacc[2];
+  if constexpr (!Elem<T>::kSplitP) {
+    sacc[0] = minit;
+    sacc[1] = minit;
+  } else {
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sacc[j][r] = 0.f;
+      for (int r = 0; r < 16; ++r) sacc[j][r] = 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < NKR; ++i) {
-    if (i + kKAhead < NKR) kread(i + kKAhead);
+    if (i + kKAhead<D, T> < NKR) kread(i + kKAhead<D, T>);
     sacc[i & 1] = Elem<T>::mfma32x32x16(__builtin_bit_cast(X8, kA[i]),
                                         __builtin_bit_cast(X8, qb[i >> 1]), sacc[i & 1]);
     __builtin_amdgcn_sched_barrier(0);
@@ -395,37 +408,82 @@ __device__ __forceinline__ void tile_math(const PrefillArgs& a, const f16* kt, c
         if (kl > rel) sacc[j][r] = -INFINITY;
       }
   }
-  float mx = -INFINITY;
+  // Two chains of three-operand maxima (v_max3_f32) over the lane's 32 keys.
+  float mx0 = fmaxf(sacc[0][0], sacc[0][1]), mx1 = fmaxf(sacc[1][0], sacc[1][1]);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sacc[0][r], sacc[1][r]));
-  mx = half_max(mx) * a.scale_log2;
-  // Lazy rescale: keep the reference max unless a score exceeds it by more
-  // than 2^8 (p stays <= 256, exact in fp16); the wave-uniform branch is
-  // taken on a row's first tile and on rare outliers only.  Only lanes whose
-  // max grows rescale (a fully masked lane keeps m_run = -inf and must not
-  // form -inf - -inf).
-  if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0 && mx > m_run) {
-    const float alpha = fast_exp2(m_run - mx);  // 0 when m_run = -inf
-    l_part *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
-    m_run = mx;
+  for (int r = 2; r < 16; r += 2) {
+    mx0 = fmaxf(fmaxf(mx0, sacc[0][r]), sacc[0][r + 1]);
+    mx1 = fmaxf(fmaxf(mx1, sacc[1][r]), sacc[1][r + 1]);
   }
-  const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
   // pb[g]: B operand for 16-key group g (keys 16g + 8(i/4) + 4hb + i%4);
   // with Elem<T>::kSplitP (bf16) p = pb + pl, two PV products.
   X8 pb[4], pl[4];
+  if constexpr (!Elem<T>::kSplitP) {
+    // rel = this tile's row max relative to m_sub.  Lazy rescale: keep the
+    // reference max unless a score exceeds it by more than 2^8 (p stays
+    // <= 256, exact in fp16); the wave-uniform branch is taken on a row's
+    // first tile and on rare outliers only.  Only lanes whose max grows
+    // rescale (a fully masked lane keeps m_run = -inf).
+    const float rel = half_max(fmaxf(mx0, mx1));
+    const bool fresh = m_run == -INFINITY;
+    if (__builtin_amdgcn_ballot_w64(rel > (fresh ? -INFINITY : kRescaleLog2)) != 0) {
+      float shift = 0.f;
+      if (rel > (fresh ? -INFINITY : 0.f)) {
+        const float m_new = rel + (fresh ? 0.f : m_run);
+        const float alpha = fast_exp2(m_run - m_new);  // 0 when m_run = -inf
+        l_part *= alpha;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+        for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
+        m_run = m_new;
+        shift = rel;
+      }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(fmaf(sacc[j][r], a.scale_log2, -m_sub));
-      pb[2 * j + (r >> 3)][r & 7] = Elem<T>::from_f(p);
-      if constexpr (Elem<T>::kSplitP)
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[j][r] -= shift;
+      const float mi = m_run == -INFINITY ? 0.f : -m_run;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) minit[r] = mi;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        pb[2 * j + (r >> 3)][r & 7] = Elem<T>::from_f(fast_exp2(sacc[j][r]));
+    // The row sum takes the probabilities as the PV product sees them (the
+    // rounded fp16 values), two per v_dot2c_f32_f16 against (1, 1).
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+    float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      l0 = __builtin_amdgcn_fdot2(h2{pb[gq][0], pb[gq][1]}, one, l0, false);
+      l1 = __builtin_amdgcn_fdot2(h2{pb[gq][2], pb[gq][3]}, one, l1, false);
+      l0 = __builtin_amdgcn_fdot2(h2{pb[gq][4], pb[gq][5]}, one, l0, false);
+      l1 = __builtin_amdgcn_fdot2(h2{pb[gq][6], pb[gq][7]}, one, l1, false);
+    }
+    l_part += l0 + l1;
+  } else {
+    const float mx = half_max(fmaxf(mx0, mx1)) * a.scale_log2;
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescaleLog2) != 0 && mx > m_run) {
+      const float alpha = fast_exp2(m_run - mx);  // 0 when m_run = -inf
+      l_part *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) acc[dt] *= alpha;
+      m_run = mx;
+    }
+    const float m_sub = (m_run == -INFINITY) ? 0.f : m_run;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(sacc[j][r], a.scale_log2, -m_sub));
+        pb[2 * j + (r >> 3)][r & 7] = Elem<T>::from_f(p);
         pl[2 * j + (r >> 3)][r & 7] =
             Elem<T>::from_f(p - Elem<T>::to_f(pb[2 * j + (r >> 3)][r & 7]));
-      l_part += p;
-    }
+        l_part += p;
+      }
+  }
   __builtin_amdgcn_sched_barrier(0);
   // O^T += V^T P^T.
 #pragma unroll
@@ -505,7 +563,20 @@ paged_prefill_kernel(PrefillArgs a) {
     for (int s = 0; s < C::NK; ++s)
       qb[s] = (ld && (!kPad || hb * (D / 2) + 8 * s < a.hd)) ? ld16(qp + 8 * s)
                                                              : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (!Elem<T>::kSplitP) {
+      // fp16: Q prescaled by scale*log2(e), rounded once to fp16.
+#pragma unroll
+      for (int s = 0; s < C::NK; ++s) {
+        f16x8 h = __builtin_bit_cast(f16x8, qb[s]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = static_cast<f16>(static_cast<float>(h[e]) * a.scale_log2);
+        qb[s] = __builtin_bit_cast(u32x4, h);
+      }
+    }
   }
+  f32x16 minit;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) minit[r] = 0.f;
 
   float m_run = -INFINITY, l_part = 0.f;
   f32x16 acc[C::NDT];
@@ -559,7 +630,7 @@ paged_prefill_kernel(PrefillArgs a) {
         if (kt + 1 < t_hi)
           tile_fetch<D, kPad>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
                         v1s);
-        if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc);
+        if (math) tile_math<D, T>(a, k0s, v0s, kt * kKT, lim, hb, L, qb, m_run, l_part, acc, minit);
         wait_all();
         __builtin_amdgcn_s_barrier();
         if (kt + 1 >= t_hi) break;
@@ -567,7 +638,7 @@ paged_prefill_kernel(PrefillArgs a) {
           tile_fetch<D, kPad>(a, bts, kbase, vbase, (kt + 2) * kKT, kv_len, wave, lane, L, win, k0s,
                         v0s);
         if (math)
-          tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc);
+          tile_math<D, T>(a, k1s, v1s, (kt + 1) * kKT, lim, hb, L, qb, m_run, l_part, acc, minit);
         wait_all();
         __builtin_amdgcn_s_barrier();
       }
