@@ -113,10 +113,16 @@ def test_argument_errors_are_reported_without_touching_the_gpu(lib):
     with pytest.raises(ValueError):
         _lib.check(st, "rmsnorm")
     p.head_size = 128
+    p.block_size = 0
+    st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
+                                        None, None, None, 0, None)
+    assert st == _lib.VAA_ERR_INVALID_ARG and "block_size=0" in _lib.last_error()
+    # Any positive block size is accepted (rows of a tile find their own
+    # blocks); the zeroed heads are what is refused next.
     p.block_size = 8
     st = lib.vaa_paged_attention_decode(ctypes.byref(p), None, None, None, None, None, None,
                                         None, None, None, 0, None)
-    assert st == _lib.VAA_ERR_UNSUPPORTED and "block_size=8" in _lib.last_error()
+    assert st == _lib.VAA_ERR_INVALID_ARG and "heads" in _lib.last_error()
 
 
 def test_zero_sized_calls_are_noops(lib):

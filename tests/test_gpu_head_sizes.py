@@ -10,58 +10,12 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, host
+from helpers import assert_close, canaried, decode_case, host, prefill_case, tail_ok
 
 import oracle.attention as oat
 import oracle.kv as okv
 
 pytestmark = pytest.mark.gpu
-
-CANARY = 0x7BCD  # an fp16 bit pattern no kernel writes here
-TAIL = 256
-
-
-def _canaried(t: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """(device buffer, view): t's contents on the GPU followed by TAIL canary
-    elements, so a write past t's last element shows in the buffer's tail."""
-    buf = torch.full((t.numel() + TAIL,), CANARY, dtype=torch.int16).view(t.dtype)
-    buf[:t.numel()] = t.reshape(-1)
-    buf = buf.cuda()
-    return buf, buf[:t.numel()].view(t.shape)
-
-
-def _tail_ok(buf: torch.Tensor) -> bool:
-    return bool((buf[-TAIL:].view(torch.int16).cpu() == CANARY).all())
-
-
-def _decode_case(S, H, KV, D, lens, layout, seed, bs=16):
-    g = torch.Generator().manual_seed(seed)
-    nblk = [(L + bs - 1) // bs for L in lens]
-    maxb = max(nblk)
-    nb = sum(nblk) + 3
-    shape = (nb, KV, bs, D) if layout == "kernel" else (nb, bs, KV, D)
-    kc = torch.randn(shape, generator=g).half()
-    vc = torch.randn(shape, generator=g).half()
-    perm = torch.randperm(nb, generator=g).to(torch.int32)
-    bt = torch.full((S, maxb), -1, dtype=torch.int32)
-    off = 0
-    for s, n in enumerate(nblk):
-        bt[s, :n] = perm[off:off + n]
-        off += n
-    # The last sequence's last block is the pool's last one, so its new token
-    # (offset 15 when L % 16 == 0) lands on the pool's last rows.
-    s_last, b_last = S - 1, nblk[-1] - 1
-    where = (bt == nb - 1).nonzero()
-    if len(where):
-        r, c = where[0].tolist()
-        bt[r, c], bt[s_last, b_last] = bt[s_last, b_last].item(), nb - 1
-    else:
-        bt[s_last, b_last] = nb - 1
-    q = torch.randn(S, H, D, generator=g).half()
-    nk = torch.randn(S, KV, D, generator=g).half()
-    nv = torch.randn(S, KV, D, generator=g).half()
-    return kc, vc, bt, torch.tensor(lens, dtype=torch.int32), q, nk, nv
-
 
 @pytest.mark.parametrize("D", [8, 40, 72, 80, 112])
 @pytest.mark.parametrize("H,KV", [(32, 8), (14, 2)])
@@ -72,16 +26,16 @@ def test_decode_padded_head_sizes(gpu, D, H, KV, layout):
     from vllm_apple_amd import kernels
 
     lens = [1, 15, 17, 300, 1000, 2096]
-    kc, vc, bt, L, q, nk, nv = _decode_case(6, H, KV, D, lens, layout, seed=D + H)
+    kc, vc, bt, L, q, nk, nv = decode_case(6, H, KV, D, lens, layout, seed=D + H)
     scale = 1.0 / np.sqrt(D)
     kr, vr = host(kc).copy(), host(vc).copy()
     okv.kv_write_decode(kr, vr, host(nk), host(nv), host(bt), host(L), layout)
     ref = oat.decode(host(q), kr, vr, host(bt), host(L), scale, layout)
     for part in (0, 128, kernels.PARTITION_BALANCED, kernels.PARTITION_BALANCED_SHARED):
         print(f"[case] decode D={D} H={H} KV={KV} {layout} part={part}", flush=True)
-        kb, kd = _canaried(kc)
-        vb, vd = _canaried(vc)
-        ob, out = _canaried(torch.zeros(q.shape, dtype=torch.float16))
+        kb, kd = canaried(kc)
+        vb, vd = canaried(vc)
+        ob, out = canaried(torch.zeros(q.shape, dtype=torch.float16))
         kernels.paged_decode(q.cuda(), kd, vd, bt.cuda(), L.cuda(), scale=scale,
                              max_seq_len=max(lens), layout=layout, output=out,
                              new_keys=nk.cuda(), new_values=nv.cuda(), partition_size=part)
@@ -89,7 +43,7 @@ def test_decode_padded_head_sizes(gpu, D, H, KV, layout):
         assert_close(host(out), ref, what=f"decode D={D} {layout} part={part}")
         assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16)), "fused K write"
         assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16)), "fused V write"
-        assert _tail_ok(kb) and _tail_ok(vb) and _tail_ok(ob), "write past the last row"
+        assert tail_ok(kb) and tail_ok(vb) and tail_ok(ob), "write past the last row"
 
 
 def test_decode_padded_unfused_and_seq_len_one(gpu):
@@ -97,7 +51,7 @@ def test_decode_padded_unfused_and_seq_len_one(gpu):
     (test_metal_kernels.py:380-438) at D = 80."""
     from vllm_apple_amd import kernels
 
-    kc, vc, bt, L, q, nk, nv = _decode_case(3, 16, 4, 80, [1, 700, 1], "kernel", seed=5)
+    kc, vc, bt, L, q, nk, nv = decode_case(3, 16, 4, 80, [1, 700, 1], "kernel", seed=5)
     out = kernels.paged_decode(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), L.cuda(),
                                scale=1 / np.sqrt(80), max_seq_len=700, new_keys=nk.cuda(),
                                new_values=nv.cuda())
@@ -115,29 +69,6 @@ def test_decode_padded_unfused_and_seq_len_one(gpu):
     assert np.array_equal(host(kd).view(np.uint16), host(kc).view(np.uint16))
 
 
-def _prefill_case(ctx, new, H, KV, D, layout, seed, bs=16):
-    g = torch.Generator().manual_seed(seed)
-    nblk = [(L + bs - 1) // bs for L in ctx]
-    nb = sum(nblk) + 2
-    maxb = max(nblk)
-    shape = (nb, KV, bs, D) if layout == "kernel" else (nb, bs, KV, D)
-    kc = torch.randn(shape, generator=g).half()
-    vc = torch.randn(shape, generator=g).half()
-    perm = torch.randperm(nb, generator=g).to(torch.int32)
-    bt = torch.full((len(ctx), maxb), -1, dtype=torch.int32)
-    off = 0
-    for s, n in enumerate(nblk):
-        bt[s, :n] = perm[off:off + n]
-        off += n
-    tok, pos = [], []
-    for s, (L, n) in enumerate(zip(ctx, new)):
-        tok += [s] * n
-        pos += list(range(L - n, L))
-    q = torch.randn(len(tok), H, D, generator=g).half()
-    return (kc, vc, bt, torch.tensor(tok, dtype=torch.int32),
-            torch.tensor(pos, dtype=torch.int32), q)
-
-
 @pytest.mark.parametrize("D", [8, 40, 80, 112])
 @pytest.mark.parametrize("H,KV", [(32, 8), (14, 2), (8, 8)])
 @pytest.mark.parametrize("layout", ["kernel", "vllm"])
@@ -147,20 +78,20 @@ def test_prefill_padded_head_sizes(gpu, D, H, KV, layout):
     from vllm_apple_amd import kernels
 
     ctx, new = [77, 1500, 40, 700], [40, 96, 40, 33]
-    kc, vc, bt, tok, pos, q = _prefill_case(ctx, new, H, KV, D, layout, seed=3 * D + H)
+    kc, vc, bt, tok, pos, q = prefill_case(ctx, new, H, KV, D, layout, seed=3 * D + H)
     scale = 1.0 / np.sqrt(D)
     ref, written = oat.prefill(host(q), host(kc), host(vc), host(bt), host(tok), host(pos),
                                scale, layout)
     assert written.all()
     for split in (0, 256):
         print(f"[case] prefill D={D} H={H} KV={KV} {layout} split={split}", flush=True)
-        ob, out = _canaried(torch.zeros(q.shape, dtype=torch.float16))
+        ob, out = canaried(torch.zeros(q.shape, dtype=torch.float16))
         kernels.paged_prefill(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), tok.cuda(), pos.cuda(),
                               scale=scale, layout=layout, output=out, split_keys=split,
                               max_seq_len=max(ctx))
         torch.cuda.synchronize()
         assert_close(host(out), ref, what=f"prefill D={D} {layout} split={split}")
-        assert _tail_ok(ob), "write past the last output row"
+        assert tail_ok(ob), "write past the last output row"
 
 
 @pytest.mark.parametrize("D", [40, 80, 112])
@@ -180,12 +111,12 @@ def test_kv_write_slots_padded_head_sizes(gpu, D):
     perm[0], perm[last] = nb * bs - 1, perm[0].item()  # the pool's last row, once
     slots = perm[:T].clone()
     slots[1::7] = -1
-    kb, kd = _canaried(kc)
-    vb, vd = _canaried(vc)
+    kb, kd = canaried(kc)
+    vb, vd = canaried(vc)
     kernels.kv_write_slots(k.cuda(), v.cuda(), kd, vd, slots.cuda())
     torch.cuda.synchronize()
     kr, vr = host(kc).copy(), host(vc).copy()
     okv.kv_write_slots(kr, vr, host(k), host(v), host(slots))
     assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
     assert np.array_equal(host(vd).view(np.uint16), vr.view(np.uint16))
-    assert _tail_ok(kb) and _tail_ok(vb)
+    assert tail_ok(kb) and tail_ok(vb)

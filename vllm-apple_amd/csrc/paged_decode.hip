@@ -102,6 +102,9 @@ struct DecodeArgs {
   float scale_log2;
   int hd;  // head size (<= D; the kPad kernels mask dims hd .. D-1)
   int num_seqs, max_blocks, block_size, num_kv_heads, num_q_heads, G;
+  // block_size is a multiple of 16, so every 16-token tile lies in one block.
+  // Otherwise (the kPad kernels only) each row of a tile finds its own block.
+  int bs16;
   int Gc, chunks;  // query heads per chunk (<= 16) and chunks per kv head
   int part_tiles, max_parts;
   int lds_main;  // bytes of LDS before the balanced split's prefix sums
@@ -184,11 +187,63 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
     t.v[i] = (!kPad || ((m.vval >> i) & 1u)) ? ld16_stream(vb + m.voff[i]) : z;
 }
 
-// One tile of math.  valid = number of real tokens in the tile (16 for every
-// tile but the sequence's last one; 0 for an invalid block).
+// A tile whose rows may lie in different blocks (block_size not a multiple
+// of 16): each row finds its physical block in the window (lane i of vals:
+// block blk0 + i) with a cross-lane read.  Returns the rows that lie in valid
+// blocks (bit r: row r); the others load row 0 of block 0 and are masked.
+template <int D, bool kStream, bool kPad>
+__device__ __forceinline__ uint32_t issue_tile_rows(const DecodeArgs& a, int64_t kbase,
+                                                    int64_t vbase, const LaneMap<D>& m,
+                                                    int vals, int blk0, int j, int lane,
+                                                    Tile<D>& t) {
+  using C = Cfg<D>;
+  const int c16 = lane & 15, g = lane >> 4;
+  auto row_at = [&](int row, int64_t& phys, int& rin) {
+    const int tok = j * kTile + row;
+    const int bi = tok / a.block_size;
+    phys = __shfl(vals, bi - blk0, kWave);
+    rin = tok - bi * a.block_size;
+    const bool ok = phys >= 0 && phys < a.num_blocks;
+    if (!ok) {
+      phys = 0;
+      rin = 0;
+    }
+    return ok;
+  };
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  int64_t pk;
+  int rk;
+  const bool kok = row_at(c16, pk, rk);
+  const f16* kp = a.kc + kbase + pk * a.k_sb + rk * a.k_st + 8 * g;
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) {
+    if (kPad && !((m.kval >> s) & 1u)) {
+      t.k[s] = z;
+      continue;
+    }
+    t.k[s] = kStream ? ld16_stream(kp + 32 * s) : ld16(kp + 32 * s);
+  }
+#pragma unroll
+  for (int i = 0; i < C::VLD; ++i) {
+    if (kPad && !((m.vval >> i) & 1u)) {
+      t.v[i] = z;
+      continue;
+    }
+    int64_t pv;
+    int rv;
+    row_at(m.vrow[i], pv, rv);
+    const int ch = (i * kWave + lane) % C::CH;
+    t.v[i] = ld16_stream(a.vc + vbase + pv * a.v_sb + rv * a.v_st + ch * 8);
+  }
+  return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(kok && g == 0)) & 0xFFFFu;
+}
+
+// One tile of math.  vmask bit r: row r of the tile is a real token of a
+// valid block (all 16 for every tile but the sequence's last one; none for
+// an invalid block).
 template <int D, typename T>
 __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
-                                          const u32x4* qb, T* vt, int valid, int g,
+                                          const u32x4* qb, T* vt, uint32_t vmask, int g,
                                           float scale_log2, float& m_run, float& l_part,
                                           f32x4* acc) {
   using C = Cfg<D>;
@@ -196,7 +251,7 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
   // contents (even NaN) can never reach the accumulators.
 #pragma unroll
   for (int i = 0; i < C::VLD; ++i) {
-    const u32x4 v = m.vrow[i] < valid ? t.v[i] : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 v = ((vmask >> m.vrow[i]) & 1u) ? t.v[i] : u32x4{0u, 0u, 0u, 0u};
     *reinterpret_cast<u32x4*>(vt + m.wlds[i]) = v;
   }
   // S^T = K Q^T.
@@ -211,7 +266,7 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
   float mx = -INFINITY;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    x[r] = (4 * g + r < valid) ? s4[r] * scale_log2 : -INFINITY;
+    x[r] = ((vmask >> (4 * g + r)) & 1u) ? s4[r] * scale_log2 : -INFINITY;
     mx = fmaxf(mx, x[r]);
   }
   mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
@@ -251,6 +306,66 @@ __device__ __forceinline__ void tile_math(const LaneMap<D>& m, const Tile<D>& t,
     acc[dt] = Elem<T>::mfma16x16x16(va, ph, acc[dt]);
     if constexpr (Elem<T>::kSplitP) acc[dt] = Elem<T>::mfma16x16x16(va, pl, acc[dt]);
   }
+}
+
+// The peeled last tile of a sequence when block_size is not a multiple of
+// 16: rows tok0 .. tok0 + nrows - 1 each read from their own block (pre, when
+// has_pre: the table entries of blocks 0-63, lane i holding entry i); the row
+// of the new token (new_row) comes from new_k/new_v and, when write_new, is
+// written to its slot in the cache.  Returns the rows that are real tokens of
+// valid blocks.
+template <int D, bool kPad>
+__device__ __forceinline__ uint32_t load_peeled_rows(const DecodeArgs& a, const LaneMap<D>& m,
+                                                     int seq, int kvh, int64_t kbase,
+                                                     int64_t vbase, int tok0, int nrows,
+                                                     int new_row, bool write_new, bool has_pre,
+                                                     int pre, int lane, Tile<D>& t) {
+  using C = Cfg<D>;
+  const int c16 = lane & 15, g = lane >> 4;
+  auto row_at = [&](int row, int64_t& phys, int& rin) {
+    const int tok = tok0 + row, bi = tok / a.block_size;
+    if (has_pre && bi < kWave)
+      phys = __shfl(pre, bi, kWave);  // -1 past max_blocks, as the table read
+    else
+      phys = bi < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi] : -1;
+    rin = tok - bi * a.block_size;
+    const bool ok = phys >= 0 && phys < a.num_blocks;
+    if (!ok) {
+      phys = 0;
+      rin = 0;
+    }
+    return ok;
+  };
+  int64_t pk;
+  int rk;
+  const bool kok = row_at(c16, pk, rk);
+  f16* krow = a.kc + kbase + pk * a.k_sb + rk * a.k_st + 8 * g;
+  const bool kmine = c16 == new_row && kok;
+  const f16* kp = kmine ? a.new_k + seq * a.n_st + kvh * a.n_sh + 8 * g : krow;
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) {
+    const bool in = !kPad || ((m.kval >> s) & 1u);
+    t.k[s] = in ? ld16(kp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    if (in && kmine && write_new) st16(krow + 32 * s, t.k[s]);
+  }
+#pragma unroll
+  for (int i = 0; i < C::VLD; ++i) {
+    if (kPad && !((m.vval >> i) & 1u)) {
+      t.v[i] = u32x4{0u, 0u, 0u, 0u};
+      continue;
+    }
+    int64_t pv;
+    int rv;
+    const bool vok = row_at(m.vrow[i], pv, rv);
+    const int ch = (i * kWave + lane) % C::CH;
+    f16* vrow = a.vc + vbase + pv * a.v_sb + rv * a.v_st + ch * 8;
+    const bool vmine = m.vrow[i] == new_row && vok;
+    const f16* vp = vmine ? a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8 : vrow;
+    t.v[i] = ld16(vp);
+    if (vmine && write_new) st16(vrow, t.v[i]);
+  }
+  return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(kok && c16 < nrows && g == 0)) &
+         0xFFFFu;
 }
 
 // Where the result of one (sequence, kv head, tile range) goes.
@@ -338,41 +453,45 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto valid_of = [&](int64_t p) { return (p < 0 || p >= a.num_blocks) ? 0 : kTile; };
   // Each chunk covers the tiles of 64 consecutive blocks (one VGPR of
-  // block-table entries).
+  // block-table entries).  With block_size not a multiple of 16 (kPad
+  // kernels only) a chunk ends at the last tile that lies wholly before the
+  // window's end.
   const bool in_pre = has_pre && jm * kTile <= kWave * a.block_size;
   for (int cb = jb; cb < jm;) {
     const int blk0 = in_pre ? 0 : (cb * kTile) / a.block_size;
     const int ce = min(jm, ((blk0 + kWave) * a.block_size) / kTile);
     const int vals = in_pre ? pre : load_window(a, seq, blk0, lane);
+    // Issues tile jj into r; returns its rows of valid blocks.
+    auto issue = [&](int jj, Tile<D>& r) -> uint32_t {
+      if (kPad && !a.bs16)
+        return issue_tile_rows<D, kStream, kPad>(a, kbase, vbase, m, vals, blk0, jj, lane, r);
+      const int64_t p = window_block(a, vals, blk0, jj);
+      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p, jj, r);
+      return (p < 0 || p >= a.num_blocks) ? 0u : 0xFFFFu;
+    };
     // Three rotating tile buffers; loads run two tiles ahead.  Prefetch
     // indices past the chunk are clamped to its last tile (an L2 hit), which
     // keeps the loop free of branches around loads.
     const int jl = ce - 1;
     Tile<D> r0, r1, r2;
-    int64_t p0 = window_block(a, vals, blk0, cb);
-    issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p0, cb, r0);
-    int64_t p1 = window_block(a, vals, blk0, min(cb + 1, jl));
-    issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p1, min(cb + 1, jl), r1);
-    int64_t p2;
+    uint32_t v0 = issue(cb, r0);
+    uint32_t v1 = issue(min(cb + 1, jl), r1);
+    uint32_t v2;
     int j = cb;
     for (; j + 3 <= ce; j += 3) {
-      p2 = window_block(a, vals, blk0, min(j + 2, jl));
-      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p2, min(j + 2, jl), r2);
-      tile_math<D, T>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
-      p0 = window_block(a, vals, blk0, min(j + 3, jl));
-      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p0, min(j + 3, jl), r0);
-      tile_math<D, T>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
-      p1 = window_block(a, vals, blk0, min(j + 4, jl));
-      issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p1, min(j + 4, jl), r1);
-      tile_math<D, T>(m, r2, qb, vt, valid_of(p2), g, a.scale_log2, m_run, l_part, acc);
+      v2 = issue(min(j + 2, jl), r2);
+      tile_math<D, T>(m, r0, qb, vt, v0, g, a.scale_log2, m_run, l_part, acc);
+      v0 = issue(min(j + 3, jl), r0);
+      tile_math<D, T>(m, r1, qb, vt, v1, g, a.scale_log2, m_run, l_part, acc);
+      v1 = issue(min(j + 4, jl), r1);
+      tile_math<D, T>(m, r2, qb, vt, v2, g, a.scale_log2, m_run, l_part, acc);
     }
     // Remainder (0..2 tiles): r0 holds tile j, r1 tile j+1.
     if (j < ce) {
-      tile_math<D, T>(m, r0, qb, vt, valid_of(p0), g, a.scale_log2, m_run, l_part, acc);
+      tile_math<D, T>(m, r0, qb, vt, v0, g, a.scale_log2, m_run, l_part, acc);
       if (j + 1 < ce)
-        tile_math<D, T>(m, r1, qb, vt, valid_of(p1), g, a.scale_log2, m_run, l_part, acc);
+        tile_math<D, T>(m, r1, qb, vt, v1, g, a.scale_log2, m_run, l_part, acc);
     }
     cb = ce;
   }
@@ -384,44 +503,50 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
   if (special >= jb && special < je) {
     const int j = special;
     const int tok0 = j * kTile;
-    const int bi = tok0 / a.block_size;
-    int64_t phys;
-    if (has_pre && bi < kWave)
-      phys = __builtin_amdgcn_readlane(pre, bi);  // -1 past max_blocks, as the table read
-    else
-      phys = bi < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi] : -1;
-    const bool bvalid = phys >= 0 && phys < a.num_blocks;
-    const int valid = bvalid ? min(kTile, L - tok0) : 0;
-    if (!bvalid) phys = 0;
     const int new_row = fused ? (L - 1) - tok0 : -1;
-    const int row0 = tok0 % a.block_size;
-    f16* kb = a.kc + kbase + phys * a.k_sb + row0 * a.k_st;
-    f16* vb = a.vc + vbase + phys * a.v_sb + row0 * a.v_st;
     Tile<D> t;
-    {
-      const bool mine = (c16 == new_row) && bvalid;
-      const f16* kp = mine ? a.new_k + seq * a.n_st + kvh * a.n_sh + 8 * g
-                           : kb + m.koff;
+    uint32_t vm;
+    if (kPad && !a.bs16) {
+      vm = load_peeled_rows<D, kPad>(a, m, seq, kvh, kbase, vbase, tok0, min(kTile, L - tok0),
+                                     new_row, write_new, has_pre, pre, lane, t);
+    } else {
+      const int bi = tok0 / a.block_size;
+      int64_t phys;
+      if (has_pre && bi < kWave)
+        phys = __builtin_amdgcn_readlane(pre, bi);  // -1 past max_blocks, as the table read
+      else
+        phys = bi < a.max_blocks ? a.bt[static_cast<int64_t>(seq) * a.max_blocks + bi] : -1;
+      const bool bvalid = phys >= 0 && phys < a.num_blocks;
+      vm = bvalid ? (1u << min(kTile, L - tok0)) - 1u : 0u;
+      if (!bvalid) phys = 0;
+      const int row0 = tok0 % a.block_size;
+      f16* kb = a.kc + kbase + phys * a.k_sb + row0 * a.k_st;
+      f16* vb = a.vc + vbase + phys * a.v_sb + row0 * a.v_st;
+      {
+        const bool mine = (c16 == new_row) && bvalid;
+        const f16* kp = mine ? a.new_k + seq * a.n_st + kvh * a.n_sh + 8 * g
+                             : kb + m.koff;
 #pragma unroll
-      for (int s = 0; s < C::NS; ++s) {
-        const bool in = !kPad || ((m.kval >> s) & 1u);
-        t.k[s] = in ? ld16(kp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-        if (in && mine && write_new) st16(kb + m.koff + 32 * s, t.k[s]);
+        for (int s = 0; s < C::NS; ++s) {
+          const bool in = !kPad || ((m.kval >> s) & 1u);
+          t.k[s] = in ? ld16(kp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+          if (in && mine && write_new) st16(kb + m.koff + 32 * s, t.k[s]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < C::VLD; ++i) {
+        if (kPad && !((m.vval >> i) & 1u)) {
+          t.v[i] = u32x4{0u, 0u, 0u, 0u};
+          continue;
+        }
+        const bool mine = (m.vrow[i] == new_row) && bvalid;
+        const int ch = (i * kWave + lane) % C::CH;
+        const f16* vp = mine ? a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8 : vb + m.voff[i];
+        t.v[i] = ld16(vp);
+        if (mine && write_new) st16(vb + m.voff[i], t.v[i]);
       }
     }
-#pragma unroll
-    for (int i = 0; i < C::VLD; ++i) {
-      if (kPad && !((m.vval >> i) & 1u)) {
-        t.v[i] = u32x4{0u, 0u, 0u, 0u};
-        continue;
-      }
-      const bool mine = (m.vrow[i] == new_row) && bvalid;
-      const int ch = (i * kWave + lane) % C::CH;
-      const f16* vp = mine ? a.new_v + seq * a.n_st + kvh * a.n_sh + ch * 8 : vb + m.voff[i];
-      t.v[i] = ld16(vp);
-      if (mine && write_new) st16(vb + m.voff[i], t.v[i]);
-    }
-    tile_math<D, T>(m, t, qb, vt, valid, g, a.scale_log2, m_run, l_part, acc);
+    tile_math<D, T>(m, t, qb, vt, vm, g, a.scale_log2, m_run, l_part, acc);
   }
 
   // Sum over the four token groups of this head.
@@ -505,7 +630,7 @@ __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int seq) {
 // ones, so that two workgroups share a CU and one's start-up (Q load, first
 // tiles) overlaps the other's tail.
 template <int D, typename T, int NW, bool kPad>
-__global__ void __launch_bounds__(NW* kWave)
+__global__ void __launch_bounds__(NW* kWave) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int part = blockIdx.y, seq = blockIdx.z;
@@ -580,7 +705,7 @@ __device__ __forceinline__ void tile_prefix(const DecodeArgs& a, int* starts, in
 }
 
 template <int D, typename T, int NW, bool kPad>
-__global__ void __launch_bounds__(NW* kWave)
+__global__ void __launch_bounds__(NW* kWave) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int c = blockIdx.x, y = blockIdx.y, nc = gridDim.x;
@@ -894,9 +1019,8 @@ int check_params(const vaa_attn_params* p, const char* what) {
   if (!head_size_ok(p->head_size))
     return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d (a multiple of 8 up to 128)", what,
                 p->head_size);
-  if (p->block_size <= 0 || p->block_size % kTile != 0)
-    return fail(VAA_ERR_UNSUPPORTED, "%s: block_size=%d must be a multiple of 16",
-                what, p->block_size);
+  if (p->block_size <= 0)
+    return fail(VAA_ERR_INVALID_ARG, "%s: block_size=%d must be positive", what, p->block_size);
   if (p->num_kv_heads <= 0 || p->num_query_heads <= 0 ||
       p->num_query_heads % p->num_kv_heads != 0 ||
       p->queries_per_kv != p->num_query_heads / p->num_kv_heads)
@@ -1050,6 +1174,7 @@ int decode_impl(const char* what, const vaa_attn_params* p, const uint16_t* quer
   a.num_seqs = p->num_seqs;
   a.max_blocks = p->max_blocks_per_seq;
   a.block_size = p->block_size;
+  a.bs16 = p->block_size % kTile == 0 ? 1 : 0;
   a.num_kv_heads = p->num_kv_heads;
   a.num_q_heads = p->num_query_heads;
   a.G = p->queries_per_kv;
@@ -1067,7 +1192,10 @@ int decode_impl(const char* what, const vaa_attn_params* p, const uint16_t* quer
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = p->dtype == VAA_DTYPE_BF16;
-  const bool pad = padded_head(p->head_size) != p->head_size;
+  // Head sizes below the computed size, and block sizes that are not a
+  // multiple of 16, run the kPad kernels (masked dims, rows that find their
+  // own blocks).
+  const bool pad = padded_head(p->head_size) != p->head_size || p->block_size % kTile != 0;
 #define VAA_DECODE_CASE(DP)                                                              \
   case DP:                                                                               \
     if (pad)                                                                             \

@@ -69,6 +69,9 @@ struct PrefillArgs {
   int hd;                     // head size (<= D; the kPad kernels mask dims hd .. D-1)
   int num_tokens, num_seqs, max_blocks, block_size, G;
   int bs_shift;               // log2(block_size) when it is a power of two, else -1
+  // block_size is a multiple of 16, so each wave's 16-key group lies in one
+  // block.  Otherwise (the kPad kernels only) each row finds its own block.
+  int bs16;
   int heads_per_wg, subtiles, head_chunks;
   int tiles_y, padded_tiles;  // logical grid rows; workgroups in use (multiple of 8)
   // Split-K over the keys (grid z): split z covers key tiles
@@ -285,6 +288,36 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>(kdst)));
   const uint32_t vl0 = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>(vdst)));
+  if constexpr (kPad) {
+    if (!a.bs16) {
+      // block_size not a multiple of 16: the group's rows may lie in several
+      // blocks; each finds its own in the window (which is moved so that it
+      // covers the group's last row).  Rows past the context or in a missing
+      // block are zeros.
+      if (k0 < kv_len) {
+        const int last = min(k0 + 15, kv_len - 1) / a.block_size;
+        if (last >= w.base + kWave) window_load(a, bts, k0 / a.block_size, w);
+      }
+      const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int q = 0; q < C::NI; ++q) {
+        const int tok = k0 + L.row[q];
+        const int bq = min(tok, kv_len - 1) / a.block_size;
+        const int64_t ph = __shfl(w.vals, max(0, min(kWave - 1, bq - w.base)), kWave);
+        const bool ok = tok < kv_len && ph >= 0 && ph < a.num_blocks;
+        const int64_t rin = tok - static_cast<int64_t>(bq) * a.block_size;
+        const char* kr = kbase + 2 * (ph * a.k_sb + rin * a.k_st) +
+                         (L.koff[q] - static_cast<uint32_t>(L.row[q] * a.k_st * 2));
+        const char* vr = vbase + 2 * (ph * a.v_sb + rin * a.v_st) +
+                         (L.voff[q] - static_cast<uint32_t>(L.row[q] * a.v_st * 2));
+        if (ok && ((L.kval >> q) & 1u)) dma16(kr, kl0 + 1024 * q);
+        else *reinterpret_cast<u32x4*>(kdst + 1024 * q + 16 * lane) = z;
+        if (ok && ((L.vval >> q) & 1u)) dma16(vr, vl0 + 1024 * q);
+        else *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
+      }
+      return;
+    }
+  }
   if (nvalid > 0) {
     const char* kb = kbase + 2 * (mine * a.k_sb + static_cast<int64_t>(row0) * a.k_st);
     const char* vb = vbase + 2 * (mine * a.v_sb + static_cast<int64_t>(row0) * a.v_st);
@@ -826,9 +859,6 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
       p->max_blocks_per_seq <= 0 || p->num_blocks <= 0 || p->num_seqs < 0 ||
       num_tokens < 0)
     return fail(VAA_ERR_INVALID_ARG, "%s: bad shape params", what);
-  if (p->block_size % 16 != 0)
-    return fail(VAA_ERR_UNSUPPORTED, "%s: block_size=%d is not a multiple of 16", what,
-                p->block_size);
   if (!valid_dtype(p->dtype))
     return fail(VAA_ERR_UNSUPPORTED, "%s: dtype=%d", what, p->dtype);
   if (p->num_query_heads > 65535)
@@ -884,8 +914,9 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
   a.max_blocks = p->max_blocks_per_seq;
   a.block_size = p->block_size;
   a.bs_shift = -1;
-  for (int sh = 4; sh < 31; ++sh)
+  for (int sh = 0; sh < 31; ++sh)
     if (p->block_size == (1 << sh)) a.bs_shift = sh;
+  a.bs16 = p->block_size % 16 == 0 ? 1 : 0;
   a.G = p->queries_per_kv;
   // Waves = (token subtile, head) pairs: 4 heads x 32 tokens when the group
   // has >= 3 heads, 2 x 64 for pairs, 1 x 128 for MHA.
@@ -904,7 +935,9 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
   a.o_st = p->o_stride_token; a.o_sh = p->o_stride_head;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = p->dtype == VAA_DTYPE_BF16;
-  const bool pad = padded_head(p->head_size) != p->head_size;
+  // Head sizes below the computed size, and block sizes that are not a
+  // multiple of 16, run the kPad kernels.
+  const bool pad = padded_head(p->head_size) != p->head_size || p->block_size % 16 != 0;
 #define VAA_PREFILL_CASE(DP)                                                 \
   case DP:                                                                   \
     if (pad)                                                                 \
