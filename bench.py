@@ -45,6 +45,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefix", type=int, default=2048,
+                    help="C3: cached tokens before each 512-token chunk (2048 = the config)")
+    ap.add_argument("--tokens", type=int, default=2104,
+                    help="C5mlp: tokens of the gate/up projection (2104 = the C5 step)")
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "C1", "C2u", "C3", "C4", "C5", "C5mlp", "C2bf16", "topk",
                              "C3-launches", "all"],
@@ -439,7 +443,7 @@ def wl_c3(args) -> dict:
 
     from vllm_apple_amd import kernels, workloads
 
-    b = workloads.c3_prefill(device=torch.device("cuda:0"))
+    b = workloads.c3_prefill(device=torch.device("cuda:0"), cached=args.prefix)
     out = torch.empty_like(b.query)
     # KV write: each rotation copy has its own new K/V and its own cache.
     T = b.query.shape[0]
@@ -453,12 +457,13 @@ def wl_c3(args) -> dict:
                                                 b.token_to_seq, b.positions, scale=b.scale,
                                                 output=out), args.steps, args.warmup)
     fl = _prefill_flops(b)
-    bb = workloads.c3_prefill(device=torch.device("cuda:0"), dtype=torch.bfloat16)
+    bb = workloads.c3_prefill(device=torch.device("cuda:0"), dtype=torch.bfloat16,
+                              cached=args.prefix)
     out_b = torch.empty_like(bb.query)
     t_bf = _timed(lambda: kernels.paged_prefill(bb.query, bb.k_cache, bb.v_cache, bb.block_table,
                                                 bb.token_to_seq, bb.positions, scale=bb.scale,
                                                 output=out_b), args.steps, args.warmup)
-    rec = {"workload": "C3", "note": "4 x (2048 cached + 512 new), causal chunk",
+    rec = {"workload": "C3", "note": f"4 x ({args.prefix} cached + 512 new), causal chunk",
             "tokens": T, "kv_write_ms": round(t_kv, 5),
             "kv_write_gb_s": round(kv_bytes / (t_kv * 1e-3) / 1e9, 1),
             "kv_write_copy_floor": _vs_copy(t_kv, kv_bytes, args.steps, args.warmup),
@@ -684,7 +689,7 @@ def wl_c2bf16(args) -> dict:
 
 def wl_c5mlp(args) -> dict:
     """C5's SwiGLU with its producer: the gated MLP's up projection
-    (2104 tokens, hidden 5120, intermediate 32768; x N(0,1), the fused
+    (2104 tokens, or --tokens, hidden 5120, intermediate 32768; x N(0,1), the fused
     gate_up weight [65536, 5120] N(0, 1/5120)) with the SiLU*mul epilogue in
     one MFMA kernel, against the reference's order on this GPU: the
     projection as a library GEMM (torch.matmul, hipBLASLt) into a [T, 2I]
@@ -694,7 +699,7 @@ def wl_c5mlp(args) -> dict:
     from vllm_apple_amd import kernels
 
     dev = torch.device("cuda:0")
-    T, H, I = 2104, 5120, 32768
+    T, H, I = args.tokens, 5120, 32768
     g = torch.Generator(device=dev).manual_seed(55)
     x = torch.randn(T, H, generator=g, device=dev).half()
     w = (torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).half()
@@ -710,7 +715,7 @@ def wl_c5mlp(args) -> dict:
     t_unfused = _timed(unfused, args.steps, args.warmup)
     flops = 2.0 * T * H * 2 * I
     tf = flops / (t_fused * 1e-3) / 1e12
-    return {"workload": "C5mlp", "note": "gate_up projection + SwiGLU, 2104 x 5120 -> 2 x 32768",
+    return {"workload": "C5mlp", "note": f"gate_up projection + SwiGLU, {T} x 5120 -> 2 x 32768",
             "flops": flops,
             "gate_up_silu_ms": round(t_fused, 5), "gate_up_silu_tflops": round(tf, 1),
             "pct_mfma_peak_f16": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 2),

@@ -96,6 +96,32 @@ def test_forward_mixed_batch_vllm_cache(gpu):
     assert_close(host(out), ref, what="forward mixed")
 
 
+@pytest.mark.parametrize("bs", [8, 12, 32])
+def test_forward_mixed_batch_block_sizes(gpu, bs):
+    """forward on a vLLM cache whose block size is not 16 (the platform
+    selects this backend for any block size, as the reference's does): KV
+    write bit-exact, decode and prefill rows against the oracle."""
+    from vllm_apple_amd.backend import HipAttentionImpl
+
+    b = _mixed_batch(bs=bs, seed=11 + bs)
+    H, KV, D, T = b["H"], b["KV"], b["D"], b["T"]
+    scale = 1 / math.sqrt(D)
+    impl = HipAttentionImpl(H, D, scale, KV, None, None, "auto")
+    dev = torch.device("cuda")
+    qkv = b["qkv"].to(dev)
+    q = qkv[:, :H * D].view(T, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(T, KV, D)
+    v = qkv[:, (H + KV) * D:].view(T, KV, D)
+    kv_cache = b["kv_cache"].to(dev)
+    out = torch.zeros((T, H, D), dtype=torch.float16, device=dev)
+    impl.forward(None, q, k, v, kv_cache, _metadata(b, dev), output=out)
+    torch.cuda.synchronize()
+    ref, kc, vc = _oracle(b, scale)
+    assert np.array_equal(host(kv_cache[0]).view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(host(kv_cache[1]).view(np.uint16), vc.view(np.uint16))
+    assert_close(host(out), ref, what=f"forward bs={bs}")
+
+
 @pytest.mark.parametrize("H,KV", [(48, 1), (40, 2)])
 def test_forward_mixed_batch_wide_groups(gpu, H, KV):
     """A layer whose GQA group has more than 16 query heads (MQA with 48

@@ -16,7 +16,7 @@ def test_supported_layers_get_the_hip_backend(monkeypatch):
     monkeypatch.delenv(P.ATTENTION_ENV, raising=False)
     for hs in (32, 64, 96, 128):
         for dt in (torch.float16, torch.bfloat16):
-            for bs in (16, 32, 128):
+            for bs in (8, 12, 16, 32, 128):
                 assert sel(head_size=hs, dtype=dt, block_size=bs) == P.BACKEND_CLS
     assert sel(kv_cache_dtype=None) == P.BACKEND_CLS
     assert P.HipAttentionPlatformMixin.get_attn_backend_cls(
@@ -27,7 +27,7 @@ def test_unsupported_layers_fall_back(monkeypatch):
     monkeypatch.delenv(P.ATTENTION_ENV, raising=False)
     monkeypatch.delenv(P.FALLBACK_ENV, raising=False)
     for kw in (dict(head_size=256), dict(head_size=80), dict(dtype=torch.float32),
-               dict(kv_cache_dtype="fp8_e4m3"), dict(has_sink=True), dict(block_size=8)):
+               dict(kv_cache_dtype="fp8_e4m3"), dict(has_sink=True)):
         assert sel(**kw) == P.DEFAULT_FALLBACK, kw
     monkeypatch.setenv(P.FALLBACK_ENV, "my.backend.Cls")
     assert sel(head_size=256) == "my.backend.Cls"

@@ -13,9 +13,9 @@ that class when vLLM is importable, and the plugin entry point
 Differences from the reference's rule: our backend is on unless
 VLLM_VAA_ATTENTION=0, and it also steps aside for what its kernels do not
 implement: FP8 KV caches (the reference's impl raises for them,
-metal_attn.py:387-388), attention sinks, and block sizes that are not a
-multiple of 16.  The fallback is VLLM_VAA_FALLBACK_BACKEND, by default vLLM's
-Triton backend on ROCm.
+metal_attn.py:387-388) and attention sinks.  Any block size is accepted, as
+there.  The fallback is VLLM_VAA_FALLBACK_BACKEND, by default vLLM's Triton
+backend on ROCm.
 """
 from __future__ import annotations
 
@@ -60,8 +60,6 @@ def select_attn_backend(head_size: int, dtype: torch.dtype, kv_cache_dtype: Opti
         return _fallback(f"kv_cache_dtype={kv_cache_dtype}")
     if has_sink:
         return _fallback("attention sinks")
-    if block_size % 16 != 0:
-        return _fallback(f"block_size={block_size} is not a multiple of 16")
     logger.info("Using the HIP paged-attention backend (head_size=%d, block_size=%d, %s)",
                 head_size, block_size, dtype)
     return BACKEND_CLS
