@@ -59,14 +59,15 @@ enum { VAA_DTYPE_F16 = 0, VAA_DTYPE_BF16 = 1 };
  * vaa_attn_params.partition_size for decode:
  *   > 0  fixed split-K partitions of that many tokens (a multiple of 128);
  *   0    automatic, from max_seq_len alone;
- *   VAA_PARTITION_BALANCED  one workgroup per CU, each taking an equal share
- *        of the 16-token tiles of all sequences, split on the device from
- *        seq_lens (for unequal lengths; at most 8192 sequences).
- *   VAA_PARTITION_BALANCED_SHARED  the same split over workgroups of half the
- *        size, four per CU, for a decode that runs concurrently with another
- *        kernel (a mixed step's prefill on a second stream): its workgroups
- *        then share CUs with the other kernel's instead of waiting for them.
- *        Slower than VAA_PARTITION_BALANCED when decode runs alone.
+ *   VAA_PARTITION_BALANCED  4-wave workgroups, two per CU's worth, each
+ *        taking an equal share of the 16-token tiles of all sequences, split
+ *        on the device from seq_lens (for unequal lengths; at most 8192
+ *        sequences).
+ *   VAA_PARTITION_BALANCED_SHARED  the same split with four workgroups per
+ *        CU's worth, for a decode that runs concurrently with another kernel
+ *        (a mixed step's prefill on a second stream): its smaller shares
+ *        then fill the CUs the other kernel leaves.  A little slower than
+ *        VAA_PARTITION_BALANCED when decode runs alone.
  */
 #define VAA_PARTITION_BALANCED (-1)
 #define VAA_PARTITION_BALANCED_SHARED (-2)

@@ -120,3 +120,53 @@ def test_prefill_block_sizes_missing_block(gpu, bs):
         o = host(out)
         assert_close(o[written], ref[written], what=f"prefill missing block bs={bs}")
         assert (o[~written] == 3.0).all(), "rows reaching the missing block were written"
+
+
+def _bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.float16).numpy()
+
+
+def _bf16_from_bits(a: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(a.copy()).view(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("bs", [8, 24])
+def test_bf16_block_sizes(gpu, bs):
+    """bf16 caches at block sizes that are not a multiple of 16: fused-write
+    decode in every split mode and prefill with the key split, against the
+    fp64 oracle on the bf16 values (the bound plus the bf16 output rounding)."""
+    from helpers import assert_close_bf16
+    from vllm_apple_amd import kernels
+
+    lens = [1, 17, 300, 1000, 2096]
+    kc, vc, bt, L, q, nk, nv = decode_case(5, 32, 8, 128, lens, "kernel", seed=bs, bs=bs)
+    kc, vc, q, nk, nv = (t.bfloat16() for t in (kc, vc, q, nk, nv))
+    scale = 1.0 / np.sqrt(128)
+    kr, vr = _bf16_bits(kc).copy(), _bf16_bits(vc).copy()
+    okv.kv_write_decode(kr, vr, _bf16_bits(nk), _bf16_bits(nv), host(bt), host(L), "kernel")
+    ref = oat.decode(q.float().numpy(), _bf16_from_bits(kr), _bf16_from_bits(vr), host(bt),
+                     host(L), scale, "kernel")
+    for part in (0, 128, kernels.PARTITION_BALANCED):
+        print(f"[case] bf16 decode bs={bs} part={part}", flush=True)
+        kd, vd = kc.cuda(), vc.cuda()
+        out = kernels.paged_decode(q.cuda(), kd, vd, bt.cuda(), L.cuda(), scale=scale,
+                                   max_seq_len=max(lens), new_keys=nk.cuda(),
+                                   new_values=nv.cuda(), partition_size=part)
+        torch.cuda.synchronize()
+        assert_close_bf16(out.float().cpu().numpy(), ref, what=f"bf16 decode bs={bs} part={part}")
+        assert np.array_equal(_bf16_bits(kd).view(np.uint16), kr.view(np.uint16)), "fused K"
+        assert np.array_equal(_bf16_bits(vd).view(np.uint16), vr.view(np.uint16)), "fused V"
+
+    ctx, new = [77, 1500, 700], [40, 96, 33]
+    kc, vc, bt, tok, pos, q = prefill_case(ctx, new, 32, 8, 128, "kernel", seed=bs + 1, bs=bs)
+    kc, vc, q = kc.bfloat16(), vc.bfloat16(), q.bfloat16()
+    ref, written = oat.prefill(q.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                               host(bt), host(tok), host(pos), scale, "kernel")
+    assert written.all()
+    for split in (0, 256):
+        print(f"[case] bf16 prefill bs={bs} split={split}", flush=True)
+        out = kernels.paged_prefill(q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), tok.cuda(),
+                                    pos.cuda(), scale=scale, split_keys=split,
+                                    max_seq_len=max(ctx))
+        torch.cuda.synchronize()
+        assert_close_bf16(out.float().cpu().numpy(), ref, what=f"bf16 prefill bs={bs}")

@@ -73,10 +73,14 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;   // waves per workgroup
 constexpr int kShortPartTiles = 64;  // fixed partitions up to 1024 tokens run 4-wave workgroups
-constexpr int kSharedWaves = kWaves / 2;  // VAA_PARTITION_BALANCED_SHARED: 4-wave workgroups,
-constexpr int kSharedPerCu = 4;           // four per CU's worth of the split (C5 step beside
-                                          // the prefill: 3, 4, 6, 8 -> 0.577, 0.571, 0.579,
-                                          // 0.587 ms; two: 0.597)
+// Balanced split: 4-wave workgroups, two per CU's worth of the split alone
+// (C2u 0.115 -> 0.105 ms and C4 0.575 -> 0.547 ms against one 8-wave workgroup
+// per CU, one box), four per CU's worth for VAA_PARTITION_BALANCED_SHARED
+// beside a concurrent kernel (C5 step beside the prefill: 3, 4, 6, 8 ->
+// 0.577, 0.571, 0.579, 0.587 ms; two: 0.597).
+constexpr int kBalWaves = kWaves / 2;
+constexpr int kBalPerCu = 2;
+constexpr int kSharedPerCu = 4;
 constexpr int kTile = 16;   // tokens per MFMA tile
 
 // Tensors are raw 16-bit storage; the kernels' element type T (fp16 or bf16)
@@ -740,7 +744,7 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(y) * (nc + B) + c + seq) * a.Gc;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T, NW, NW != kSharedWaves, kPad>(a, smem, seq, kvh, qh0, nh, L,
+    decode_range<D, T, NW, false, kPad>(a, smem, seq, kvh, qh0, nh, L,
                            a.new_k != nullptr && a.seq_lens[seq] == L, hc == 0, t0, t1, ro,
                            true);
     pos = s0 + t1;
@@ -940,7 +944,7 @@ inline int heads_per_chunk(int G) {
 // How a call splits its sequences.
 struct Split {
   bool balanced;     // balanced split over the actual lengths
-  bool shared;       // balanced over 4-wave workgroups, kSharedPerCu per CU
+  bool shared;       // balanced, kSharedPerCu (else kBalPerCu) workgroups per CU's worth
   int part;          // fixed: tokens per partition (balanced: -1)
   int max_parts;     // fixed: partitions per sequence; balanced: workgroups per kv head
                      // and head chunk
@@ -951,10 +955,10 @@ struct Split {
 // Fixed partitions with partition_size > 0; with 0 the size comes from
 // max_seq_len alone (all sequences assumed at the maximum): split only as far
 // as needed for the workgroups to cover every CU once, in multiples of
-// 16 * kWaves tokens.  VAA_PARTITION_BALANCED: one workgroup per CU, each
-// taking an equal share of the tiles of all sequences (split on the device
-// from seq_lens); VAA_PARTITION_BALANCED_SHARED: the same over two 4-wave
-// workgroups per CU.
+// 16 * kWaves tokens.  VAA_PARTITION_BALANCED: 4-wave workgroups, two per
+// CU's worth, each taking an equal share of the tiles of all sequences (split
+// on the device from seq_lens); VAA_PARTITION_BALANCED_SHARED: the same with
+// four per CU's worth.
 int plan_split(const vaa_attn_params* p, Split* sp) {
   const int64_t cap = static_cast<int64_t>(p->max_blocks_per_seq) * p->block_size;
   int64_t max_len = p->max_seq_len;
@@ -968,7 +972,7 @@ int plan_split(const vaa_attn_params* p, Split* sp) {
       return fail(VAA_ERR_UNSUPPORTED, "balanced split: num_seqs=%d > %d", p->num_seqs,
                   kBalMaxSeqs);
     const bool shared = part == VAA_PARTITION_BALANCED_SHARED;
-    const int per_cu = shared ? kSharedPerCu : 1;
+    const int per_cu = shared ? kSharedPerCu : kBalPerCu;
     const int ys = p->num_kv_heads * head_chunks(p->queries_per_kv);
     const int wgs = (per_cu * num_cus() + ys - 1) / ys;
     sp->balanced = true;
@@ -1056,21 +1060,15 @@ int launch_decode(const DecodeArgs& a0, bool balanced, bool shared, hipStream_t 
       (2 * kWaves * 16 + static_cast<size_t>(kWaves) * a.Gc * D) * sizeof(float);
   const size_t lds = lds_tiles > lds_comb ? lds_tiles : lds_comb;
   if (balanced) {
-    const int nw = shared ? kSharedWaves : kWaves;
     const size_t lds_bal =
-        std::max(static_cast<size_t>(nw) * kTile * D * sizeof(f16),
-                 (2 * nw * 16 + static_cast<size_t>(nw) * a.Gc * D) * sizeof(float));
+        std::max(static_cast<size_t>(kBalWaves) * kTile * D * sizeof(f16),
+                 (2 * kBalWaves * 16 + static_cast<size_t>(kBalWaves) * a.Gc * D) * sizeof(float));
     a.lds_main = static_cast<int>((lds_bal + 15) / 16 * 16);
-    const size_t lds_b = a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kWaves) * sizeof(int);
-    if (shared)
-      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kSharedWaves, kPad>),
-                         dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kSharedWaves * kWave),
-                         lds_b,
-                         stream, a);
-    else
-      hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kWaves, kPad>),
-                         dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kWaves * kWave), lds_b,
-                         stream, a);
+    const size_t lds_b =
+        a.lds_main + (static_cast<size_t>(a.num_seqs) + 1 + kBalWaves) * sizeof(int);
+    hipLaunchKernelGGL((paged_decode_balanced_kernel<D, T, kBalWaves, kPad>),
+                       dim3(a.max_parts, a.num_kv_heads * a.chunks), dim3(kBalWaves * kWave),
+                       lds_b, stream, a);
     int st = check_launch("paged_decode_balanced_kernel");
     if (st) return st;
     hipLaunchKernelGGL((paged_decode_merge_balanced_kernel<D, T>),

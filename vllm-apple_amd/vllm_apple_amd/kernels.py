@@ -290,9 +290,10 @@ def decode_workspace_size(p: _lib.VaaAttnParams) -> tuple[int, int]:
 
 # Decode launch geometry (paged_decode.hip): partitions in multiples of 128
 # tokens; partitions up to 1024 tokens run 4-wave workgroups, two per CU (one's
-# start-up overlaps the other's streaming), longer ones and the balanced split
-# one 8-wave workgroup per CU.  The balanced split gives each workgroup at
-# least 32 tiles (512 tokens) and takes at most 8192 sequences.
+# start-up overlaps the other's streaming), longer ones one 8-wave workgroup
+# per CU.  The balanced split runs 4-wave workgroups, two per CU's worth (four
+# for the shared split), gives each workgroup at least 32 tiles (512 tokens)
+# and takes at most 8192 sequences.
 _DECODE_QUANTUM = 128
 _SHORT_PART_TOKENS = 1024
 # How much faster than its share of HBM a decode workgroup streams when the
@@ -371,9 +372,11 @@ def choose_partition_size(seq_lens_host, num_kv_heads: int, num_cus: int,
     i = int(np.argmin(t))
     best, t_fix = int(P[i]), float(t[i])
     if lens.size <= _BALANCED_MAX_SEQS:
-        c = (m + num_kv_heads - 1) // num_kv_heads
+        # Two workgroups per CU's worth share the CU: each streams half its
+        # share while the other's start-up overlaps it.
+        c = 2 * ((m + num_kv_heads - 1) // num_kv_heads)
         per = max(total / (c * num_kv_heads), float(_BALANCED_MIN_TOKENS))
-        t_bal = per + wg_tokens * (1.0 + lens.size / c) + merge_tokens
+        t_bal = 2 * per + wg_tokens * (1.0 + lens.size / c) + merge_tokens
         if t_bal < 0.97 * t_fix:
             best = PARTITION_BALANCED
     if len(_partition_cache) > 4096:
