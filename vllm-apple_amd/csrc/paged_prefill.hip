@@ -84,6 +84,10 @@ struct PrefillArgs {
   float* ws_acc;
   float* ws_ml;
   int64_t num_blocks;
+  // Byte strides in 32 bits (narrow = 1 when the block strides fit 32 bits and
+  // a block's token offsets 31): the full-group fast path of the fetch.
+  int narrow;
+  uint32_t ksb2, vsb2, kst2, vst2;
   int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
   int64_t q_st, q_sh, o_st, o_sh;
 };
@@ -167,6 +171,14 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(g), "s"(lds)
+               : "memory", "m0");
+}
+// The same from a wave-uniform base address (an SGPR pair) plus each lane's
+// 32-bit byte offset: no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 
@@ -274,6 +286,33 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
                                            BlockWindow& w, f16* kd, f16* vd) {
   using C = PCfg<D>;
   const int k0 = key0 + 16 * wave;
+  if constexpr (!kPad) {
+    // Full 16-key group in a valid block (every group but a sequence's
+    // last): one window read, a 32-bit offset product per half and eight
+    // direct loads from a wave-uniform base.
+    if (a.narrow && k0 + 16 <= kv_len) {
+      const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
+      if (bi >= w.base + kWave) window_load(a, bts, bi, w);
+      const int phys = __builtin_amdgcn_readlane(w.vals, bi - w.base);
+      if (phys >= 0 && phys < a.num_blocks) {
+        const uint32_t row0 = static_cast<uint32_t>(k0 - bi * a.block_size);
+        const char* kb = kbase + static_cast<uint64_t>(static_cast<uint32_t>(phys)) * a.ksb2 +
+                         row0 * a.kst2;
+        const char* vb = vbase + static_cast<uint64_t>(static_cast<uint32_t>(phys)) * a.vsb2 +
+                         row0 * a.vst2;
+        const uint32_t kl = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+            reinterpret_cast<uintptr_t>(kd) + 1024 * (wave * C::NI)));
+        const uint32_t vl = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+            reinterpret_cast<uintptr_t>(vd) + 1024 * (wave * C::NI)));
+#pragma unroll
+        for (int q = 0; q < C::NI; ++q) {
+          dma16s(kb, L.koff[q], kl + 1024 * q);
+          dma16s(vb, L.voff[q], vl + 1024 * q);
+        }
+        return;
+      }
+    }
+  }
   int nvalid = 0, row0 = 0;
   int64_t mine = -1;
   if (k0 < kv_len) {
@@ -332,8 +371,8 @@ __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* 
           if ((L.vval >> q) & 1u) dma16(vb + L.voff[q], vl0 + 1024 * q);
           else *reinterpret_cast<u32x4*>(vdst + 1024 * q + 16 * lane) = z;
         } else {
-          dma16(kb + L.koff[q], kl0 + 1024 * q);
-          dma16(vb + L.voff[q], vl0 + 1024 * q);
+          dma16s(kb, L.koff[q], kl0 + 1024 * q);
+          dma16s(vb, L.voff[q], vl0 + 1024 * q);
         }
       }
       return;
@@ -929,6 +968,18 @@ int prefill_impl(const char* what, const vaa_attn_params* p, const uint16_t* que
   }
   a.head_chunks = (a.G + a.heads_per_wg - 1) / a.heads_per_wg;
   a.num_blocks = p->num_blocks;
+  {
+    const int64_t bs = p->block_size;
+    const bool fits = p->k_stride_block * 2 < (int64_t(1) << 32) &&
+                      p->v_stride_block * 2 < (int64_t(1) << 32) &&
+                      p->k_stride_token * 2 * bs < (int64_t(1) << 31) &&
+                      p->v_stride_token * 2 * bs < (int64_t(1) << 31);
+    a.narrow = fits ? 1 : 0;
+    a.ksb2 = fits ? static_cast<uint32_t>(p->k_stride_block * 2) : 0u;
+    a.vsb2 = fits ? static_cast<uint32_t>(p->v_stride_block * 2) : 0u;
+    a.kst2 = fits ? static_cast<uint32_t>(p->k_stride_token * 2) : 0u;
+    a.vst2 = fits ? static_cast<uint32_t>(p->v_stride_token * 2) : 0u;
+  }
   a.k_sb = p->k_stride_block; a.k_sh = p->k_stride_head; a.k_st = p->k_stride_token;
   a.v_sb = p->v_stride_block; a.v_sh = p->v_stride_head; a.v_st = p->v_stride_token;
   a.q_st = p->q_stride_token; a.q_sh = p->q_stride_head;
