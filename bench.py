@@ -47,6 +47,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prefix", type=int, default=2048,
                     help="C3: cached tokens before each 512-token chunk (2048 = the config)")
+    ap.add_argument("--split-keys", type=int, default=0,
+                    help="C3: also time the prefill split into key pieces of this many keys "
+                         "(a multiple of 64; 0 = unsplit only)")
     ap.add_argument("--tokens", type=int, default=2104,
                     help="C5mlp: tokens of the gate/up projection (2104 = the C5 step)")
     ap.add_argument("--workload", default="headline",
@@ -472,6 +475,14 @@ def wl_c3(args) -> dict:
             "mfma_util_pct": round(100 * fl / (t_at * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 2),
             "bf16_prefill_ms": round(t_bf, 5),
             "bf16_tflop_s": round(fl / (t_bf * 1e-3) / 1e12, 1)}
+    if args.split_keys:
+        t_sp = _timed(lambda: kernels.paged_prefill(b.query, b.k_cache, b.v_cache, b.block_table,
+                                                    b.token_to_seq, b.positions, scale=b.scale,
+                                                    output=out, split_keys=args.split_keys,
+                                                    max_seq_len=args.prefix + 512),
+                      args.steps, args.warmup)
+        rec["split_keys"] = args.split_keys
+        rec["prefill_split_ms"] = round(t_sp, 5)
     if not args.no_cpu_baseline:
         _cpu_threads()
         h = HostStep(b)
