@@ -164,3 +164,44 @@ def test_prefill_after_slot_write_c3_flow(gpu):
     assert np.array_equal(host(kd).view(np.uint16), kr.view(np.uint16))
     ref, w = oat.prefill(host(q), kr, vr, host(bt), host(tok), host(pos), 1 / np.sqrt(128))
     assert_close(host(out), ref, what="C3 flow")
+
+
+def test_prefill_and_decode_block_stride_past_32_bits(gpu):
+    """Caches whose block stride is 2^31 elements (4 GiB): the prefill's
+    fetch takes its 64-bit address path (the 32-bit fast path needs the byte
+    strides to fit 32 bits), and decode reads the same views; both against
+    the oracle on compact host copies of the two blocks."""
+    from vllm_apple_amd import kernels
+
+    print("[case] prefill/decode, block stride 2^31 elements", flush=True)
+    KV, bs, D, H = 2, 16, 64, 8
+    sb = 1 << 31
+    g = torch.Generator().manual_seed(21)
+    kh = torch.randn(2, KV, bs, D, generator=g).half()
+    vh = torch.randn(2, KV, bs, D, generator=g).half()
+    bufs = []
+    views = []
+    for h_ in (kh, vh):
+        buf = torch.empty(sb + KV * bs * D, dtype=torch.float16, device="cuda")
+        v = buf.as_strided((2, KV, bs, D), (sb, bs * D, D, 1))
+        v.copy_(h_.cuda())
+        bufs.append(buf)
+        views.append(v)
+    kc, vc = views
+    bt = torch.tensor([[1, 0]], dtype=torch.int32)
+    tok = torch.zeros(20, dtype=torch.int32)
+    pos = torch.arange(12, 32, dtype=torch.int32)
+    q = torch.randn(20, H, D, generator=g).half()
+    scale = 1.0 / np.sqrt(D)
+    out = kernels.paged_prefill(q.cuda(), kc, vc, bt.cuda(), tok.cuda(), pos.cuda(), scale=scale)
+    qd = torch.randn(1, H, D, generator=g).half()
+    outd = kernels.paged_decode(qd.cuda(), kc, vc, bt.cuda(), torch.tensor([29], dtype=torch.int32,
+                                device="cuda"), scale=scale, max_seq_len=29)
+    torch.cuda.synchronize()
+    ref, w = oat.prefill(host(q), host(kh), host(vh), host(bt), host(tok), host(pos), scale)
+    assert w.all()
+    assert_close(host(out), ref, what="prefill, 4 GiB block stride")
+    refd = oat.decode(host(qd), host(kh), host(vh), host(bt), np.array([29], np.int32), scale)
+    assert_close(host(outd), refd, what="decode, 4 GiB block stride")
+    del bufs, views, kc, vc
+    torch.cuda.empty_cache()
