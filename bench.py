@@ -825,6 +825,22 @@ def main() -> int:
                              new_keys=b.new_k, new_values=b.new_v,
                              partition_size=args.partition)
 
+    stream = torch.cuda.current_stream()
+    # Spread of single launches (events around each launch; informational, not
+    # part of the timed region).  It runs before the warm-up: from an idle GPU
+    # this kernel needs about 150 launches to reach its steady speed (launches
+    # 5-50 run 2-3 % slower than from 150 on), so with a short warm-up the
+    # timed region would otherwise measure the clocks settling.
+    n_iso = 50
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n_iso)]
+    for e0, e1 in ev:
+        e0.record(stream)
+        step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    kern_ms = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -834,7 +850,6 @@ def main() -> int:
     # is one launch of the decode kernel (one partition per sequence, no merge
     # launch), so the region's event time / K is that kernel's average launch
     # duration, gaps between launches included.
-    stream = torch.cuda.current_stream()
     e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -846,18 +861,6 @@ def main() -> int:
     wall = time.perf_counter() - t0
     kern_avg_ms = e_start.elapsed_time(e_end) / args.steps
     ms_per_step = wall * 1e3 / args.steps
-
-    # Spread of single launches (events around each launch; informational, not
-    # part of the timed region).
-    n_iso = min(args.steps, 50)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(n_iso)]
-    for e0, e1 in ev:
-        e0.record(stream)
-        step()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    kern_ms = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
 
     alg_bytes = b.decode_algorithmic_bytes()
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
