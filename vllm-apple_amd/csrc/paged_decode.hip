@@ -59,9 +59,10 @@
 // headline: 72 -> 79 % of HBM peak on one box; the hint on the earlier K lane
 // map, 16-byte pieces 64 bytes apart, had cost 8 points); the shared
 // balanced split, which runs beside a prefill, hints V only (issue_tile).  Loads run two tiles
-// ahead of the math in a rotated three-buffer pipeline, and the wave's
-// block-table entries sit in a VGPR (one per lane) read with readlane, so the
-// steady-state loop issues no scalar memory loads.
+// ahead of the math in a rotated three-buffer pipeline (the balanced split:
+// one tile ahead in two buffers), and the wave's block-table entries sit in a
+// VGPR (one per lane) read with readlane, so the steady-state loop issues no
+// scalar memory loads.
 #include "common.h"
 
 #include <atomic>
@@ -77,7 +78,10 @@ constexpr int kShortPartTiles = 64;  // fixed partitions up to 1024 tokens run 4
 // (C2u 0.115 -> 0.105 ms and C4 0.575 -> 0.547 ms against one 8-wave workgroup
 // per CU, one box), four per CU's worth for VAA_PARTITION_BALANCED_SHARED
 // beside a concurrent kernel (C5 step beside the prefill: 3, 4, 6, 8 ->
-// 0.577, 0.571, 0.579, 0.587 ms; two: 0.597).
+// 0.577, 0.571, 0.579, 0.587 ms; two: 0.597).  Its waves load one tile ahead
+// (C2u 0.1031-0.1035 -> 0.1011-0.1014 ms against two ahead, one box; three
+// workgroups per CU's worth at three waves per SIMD: C2u the same, C4 and
+// the C5 step slower).
 constexpr int kBalWaves = kWaves / 2;
 constexpr int kBalPerCu = 2;
 constexpr int kSharedPerCu = 4;
@@ -391,7 +395,8 @@ struct RangeOut {
 // sequence's length arrived; a wave whose tiles all lie in those blocks
 // (contexts up to 64 blocks) reads its physical blocks from it, one
 // dependent global round trip fewer.
-template <int D, typename T, int NW = kWaves, bool kStream = true, bool kPad = false>
+template <int D, typename T, int NW = kWaves, bool kStream = true, bool kPad = false,
+          int kAhead = 2>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int qh0, int nh, int L, bool fused,
                                              bool write_new, int t0, int t1, const RangeOut& ro,
@@ -474,10 +479,25 @@ __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char*
       issue_tile<D, kStream, kPad>(a, kbase, vbase, m, p, jj, r);
       return (p < 0 || p >= a.num_blocks) ? 0u : 0xFFFFu;
     };
-    // Three rotating tile buffers; loads run two tiles ahead.  Prefetch
-    // indices past the chunk are clamped to its last tile (an L2 hit), which
-    // keeps the loop free of branches around loads.
+    // Prefetch indices past the chunk are clamped to its last tile (an L2
+    // hit), which keeps the loop free of branches around loads.
     const int jl = ce - 1;
+    if constexpr (kAhead == 1) {
+      // Two tile buffers; loads run one tile ahead.
+      Tile<D> r0, r1;
+      uint32_t v0 = issue(cb, r0), v1;
+      int j = cb;
+      for (; j + 2 <= ce; j += 2) {
+        v1 = issue(j + 1, r1);
+        tile_math<D, T>(m, r0, qb, vt, v0, g, a.scale_log2, m_run, l_part, acc);
+        v0 = issue(min(j + 2, jl), r0);
+        tile_math<D, T>(m, r1, qb, vt, v1, g, a.scale_log2, m_run, l_part, acc);
+      }
+      if (j < ce) tile_math<D, T>(m, r0, qb, vt, v0, g, a.scale_log2, m_run, l_part, acc);
+      cb = ce;
+      continue;
+    }
+    // Three rotating tile buffers; loads run two tiles ahead.
     Tile<D> r0, r1, r2;
     uint32_t v0 = issue(cb, r0);
     uint32_t v1 = issue(min(cb + 1, jl), r1);
@@ -744,7 +764,7 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(y) * (nc + B) + c + seq) * a.Gc;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T, NW, false, kPad>(a, smem, seq, kvh, qh0, nh, L,
+    decode_range<D, T, NW, false, kPad, 1>(a, smem, seq, kvh, qh0, nh, L,
                            a.new_k != nullptr && a.seq_lens[seq] == L, hc == 0, t0, t1, ro,
                            true);
     pos = s0 + t1;
