@@ -58,11 +58,11 @@
 // read once per call, so its loads carry the nontemporal hint (MI355X
 // headline: 72 -> 79 % of HBM peak on one box; the hint on the earlier K lane
 // map, 16-byte pieces 64 bytes apart, had cost 8 points); the shared
-// balanced split, which runs beside a prefill, hints V only (issue_tile).  Loads run two tiles
-// ahead of the math in a rotated three-buffer pipeline (the balanced split:
-// one tile ahead in two buffers), and the wave's block-table entries sit in a
-// VGPR (one per lane) read with readlane, so the steady-state loop issues no
-// scalar memory loads.
+// balanced split, which runs beside a prefill, hints V only (issue_tile).  Loads run one tile
+// ahead of the math in two buffers (the 4-wave fixed-partition kernel: two
+// tiles ahead in three rotating buffers), and the wave's block-table entries
+// sit in a VGPR (one per lane) read with readlane, so the steady-state loop
+// issues no scalar memory loads.
 #include "common.h"
 
 #include <atomic>
@@ -78,10 +78,14 @@ constexpr int kShortPartTiles = 64;  // fixed partitions up to 1024 tokens run 4
 // (C2u 0.115 -> 0.105 ms and C4 0.575 -> 0.547 ms against one 8-wave workgroup
 // per CU, one box), four per CU's worth for VAA_PARTITION_BALANCED_SHARED
 // beside a concurrent kernel (C5 step beside the prefill: 3, 4, 6, 8 ->
-// 0.577, 0.571, 0.579, 0.587 ms; two: 0.597).  Its waves load one tile ahead
-// (C2u 0.1031-0.1035 -> 0.1011-0.1014 ms against two ahead, one box; three
-// workgroups per CU's worth at three waves per SIMD: C2u the same, C4 and
-// the C5 step slower).
+// 0.577, 0.571, 0.579, 0.587 ms; two: 0.597).  Three workgroups per CU's
+// worth at three waves per SIMD: C2u the same, C4 and the C5 step slower.
+//
+// Loads run one tile ahead in the balanced and the 8-wave kernels (against
+// two ahead, one box: C2u 0.1031-0.1035 -> 0.1011-0.1014 ms, headline
+// 0.1631-0.1632 -> 0.1622-0.1623 ms, C1 7.1 -> 6.5 us) and two ahead in the
+// 4-wave fixed-partition kernel (C4 at 512-token partitions: one ahead 0.685
+// against 0.638 ms).
 constexpr int kBalWaves = kWaves / 2;
 constexpr int kBalPerCu = 2;
 constexpr int kSharedPerCu = 4;
@@ -396,7 +400,7 @@ struct RangeOut {
 // (contexts up to 64 blocks) reads its physical blocks from it, one
 // dependent global round trip fewer.
 template <int D, typename T, int NW = kWaves, bool kStream = true, bool kPad = false,
-          int kAhead = 2>
+          int kAhead = 1>
 __device__ __forceinline__ void decode_range(const DecodeArgs& a, unsigned char* smem, int seq,
                                              int kvh, int qh0, int nh, int L, bool fused,
                                              bool write_new, int t0, int t1, const RangeOut& ro,
@@ -679,7 +683,7 @@ paged_decode_kernel(DecodeArgs a) {
   ro.whole = (n_parts == 1);
   ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh0) * a.max_parts + part;
   ro.prow_step = a.max_parts;
-  decode_range<D, T, NW, true, kPad>(a, smem, seq, kvh, qh0, nh, L,
+  decode_range<D, T, NW, true, kPad, NW == 4 ? 2 : 1>(a, smem, seq, kvh, qh0, nh, L,
                          a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro, false, part == 0,
                          pre);
 }
@@ -764,7 +768,7 @@ paged_decode_balanced_kernel(DecodeArgs a) {
     ro.prow0 = (static_cast<int64_t>(y) * (nc + B) + c + seq) * a.Gc;
     ro.prow_step = 1;
     const int L = clamped_len(a, seq);
-    decode_range<D, T, NW, false, kPad, 1>(a, smem, seq, kvh, qh0, nh, L,
+    decode_range<D, T, NW, false, kPad>(a, smem, seq, kvh, qh0, nh, L,
                            a.new_k != nullptr && a.seq_lens[seq] == L, hc == 0, t0, t1, ro,
                            true);
     pos = s0 + t1;
