@@ -57,8 +57,8 @@
 // ds_read_b64_tr_b16 (one read per MFMA operand).  The K/V stream is
 // read once per call, so its loads carry the nontemporal hint (MI355X
 // headline: 72 -> 79 % of HBM peak on one box; the hint on the earlier K lane
-// map, 16-byte pieces 64 bytes apart, had cost 8 points); the shared
-// balanced split, which runs beside a prefill, hints V only (issue_tile).  Loads run one tile
+// map, 16-byte pieces 64 bytes apart, had cost 8 points); the balanced
+// split hints V only (issue_tile).  Loads run one tile
 // ahead of the math in two buffers (the 4-wave fixed-partition kernel: two
 // tiles ahead in three rotating buffers), and the wave's block-table entries
 // sit in a VGPR (one per lane) read with readlane, so the steady-state loop
@@ -172,11 +172,11 @@ __device__ __forceinline__ int64_t window_block(const DecodeArgs& a, int vals, i
 }
 
 // V rows always load with the nontemporal hint; K rows too when kStream.
-// kStream is off for the shared balanced split, which runs beside a
-// concurrent prefill: there the hint on K cost the C5 attention step 3 %
-// (0.638-0.642 against 0.610-0.612 ms with V alone hinted), while on the
-// decode alone it helps (headline 78.4-78.7 % with V alone, 78.8-79.1 % with
-// both, one box).
+// kStream is on for the fixed partitions (headline 78.4-78.7 % with V alone
+// hinted, 78.8-79.1 % with both, one box) and off for the balanced split:
+// beside a concurrent prefill the hint on K cost the C5 attention step 3 %
+// (0.638-0.642 against 0.610-0.612 ms), and on the split alone C2u (0.1051
+// against 0.1009 ms, one box).
 template <int D, bool kStream = true, bool kPad = false>
 __device__ __forceinline__ void issue_tile(const DecodeArgs& a, int64_t kbase,
                                           int64_t vbase, const LaneMap<D>& m,
