@@ -160,6 +160,22 @@ __device__ __forceinline__ typename Elem<T>::x4 lds_tr4(const f16* p) {
 // expcnt 6:4 left at its maximum, lgkmcnt 11:8): every direct load and LDS
 // access of this wave has landed.
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+// A wave-uniform 32-bit read through the scalar unit (s_load_dword, via the
+// constant address space: the block table is not written during the
+// kernel).  lgkmcnt counts it, so waiting for it does not wait for the vector
+// loads in flight, which complete in order.
+__device__ __forceinline__ int32_t scalar_load_i32(const int32_t* p) {
+  return *((const __attribute__((address_space(4))) int32_t*)(reinterpret_cast<uintptr_t>(p)));
+}
+
+// Workgroup barrier for LDS traffic only: s_waitcnt lgkmcnt(0) (vmcnt and
+// expcnt at their maxima), so outstanding global loads stay in flight.
+__device__ __forceinline__ void lds_bar() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 
 // One 16-byte direct load per lane into LDS at lds + 16 * lane, issued as
@@ -283,17 +299,24 @@ template <int D, bool kPad>
 __device__ __forceinline__ void tile_fetch(const PrefillArgs& a, const int32_t* bts,
                                            const char* kbase, const char* vbase, int key0,
                                            int kv_len, int wave, int lane, const Lanes<D>& L,
-                                           BlockWindow& w, f16* kd, f16* vd) {
+                                           BlockWindow& w, f16* kd, f16* vd,
+                                           int phys_hint = -2) {
   using C = PCfg<D>;
   const int k0 = key0 + 16 * wave;
   if constexpr (!kPad) {
     // Full 16-key group in a valid block (every group but a sequence's
     // last): one window read, a 32-bit offset product per half and eight
-    // direct loads from a wave-uniform base.
+    // direct loads from a wave-uniform base.  phys_hint (>= -1): the
+    // group's block-table entry, read by the caller.
     if (a.narrow && k0 + 16 <= kv_len) {
       const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
-      if (bi >= w.base + kWave) window_load(a, bts, bi, w);
-      const int phys = __builtin_amdgcn_readlane(w.vals, bi - w.base);
+      int phys;
+      if (phys_hint >= -1) {
+        phys = phys_hint;
+      } else {
+        if (bi >= w.base + kWave) window_load(a, bts, bi, w);
+        phys = __builtin_amdgcn_readlane(w.vals, bi - w.base);
+      }
       if (phys >= 0 && phys < a.num_blocks) {
         const uint32_t row0 = static_cast<uint32_t>(k0 - bi * a.block_size);
         const char* kb = kbase + static_cast<uint64_t>(static_cast<uint32_t>(phys)) * a.ksb2 +
@@ -617,6 +640,24 @@ paged_prefill_kernel(PrefillArgs a) {
     tseq = a.tok_seq[tok];
     tpos = a.pos[tok];
   }
+  // Q^T as B operand: lane holds Q[token qj][hb*D/2 + 8s .. +7], s < NK.
+  // Issued right after the token's sequence and position, before the rows
+  // are validated (a row past num_tokens reads the last token's row; an
+  // invalid row's scores are all masked), so the load is in flight during
+  // the sequence discovery; prescaled before the first tile's math.
+  u32x4 qb[C::NK];
+  {
+    const int qtok = min(tok, a.num_tokens - 1);
+    const f16* qp = a.q + static_cast<int64_t>(qtok) * a.q_st + head * a.q_sh + hb * (D / 2);
+#pragma unroll
+    for (int s = 0; s < C::NK; ++s) {
+      if constexpr (kPad)
+        qb[s] = (hb * (D / 2) + 8 * s < a.hd) ? ld16(qp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
+      else
+        qb[s] = ld16(qp + 8 * s);
+    }
+  }
+  bool q_ready = false;
   bool row_ok = tseq >= 0 && tseq < a.num_seqs && tpos >= 0;
   if (row_ok) {
     const int64_t nb = (static_cast<int64_t>(tpos) + a.block_size) / a.block_size;
@@ -625,27 +666,6 @@ paged_prefill_kernel(PrefillArgs a) {
   bool done = !row_ok;
   bool aborted = false;
 
-  // Q^T as B operand: lane holds Q[token qj][hb*D/2 + 8s .. +7], s < NK.
-  u32x4 qb[C::NK];
-  {
-    const bool ld = row_ok && math;
-    const f16* qp = a.q + static_cast<int64_t>(ld ? tok : 0) * a.q_st + head * a.q_sh +
-                    hb * (D / 2);
-#pragma unroll
-    for (int s = 0; s < C::NK; ++s)
-      qb[s] = (ld && (!kPad || hb * (D / 2) + 8 * s < a.hd)) ? ld16(qp + 8 * s)
-                                                             : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (!Elem<T>::kSplitP) {
-      // fp16: Q prescaled by scale*log2(e), rounded once to fp16.
-#pragma unroll
-      for (int s = 0; s < C::NK; ++s) {
-        f16x8 h = __builtin_bit_cast(f16x8, qb[s]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = static_cast<f16>(static_cast<float>(h[e]) * a.scale_log2);
-        qb[s] = __builtin_bit_cast(u32x4, h);
-      }
-    }
-  }
   f32x16 minit;
 #pragma unroll
   for (int r = 0; r < 16; ++r) minit[r] = 0.f;
@@ -666,7 +686,7 @@ paged_prefill_kernel(PrefillArgs a) {
     // Next sequence among the workgroup's unfinished tokens, and its context.
     int s = wave_min_i(done ? INT32_MAX : tseq);
     if (lane == 0) red[0][wave] = s;
-    __syncthreads();
+    lds_bar();
     s = red[0][0];
 #pragma unroll
     for (int w = 1; w < kWavesP; ++w) s = min(s, red[0][w]);
@@ -674,14 +694,13 @@ paged_prefill_kernel(PrefillArgs a) {
     const bool active = !done && tseq == s;
     int kv_len = wave_max_i(active ? tpos + 1 : 0);
     if (lane == 0) red[1][wave] = kv_len;
-    __syncthreads();
+    lds_bar();
     kv_len = red[1][0];
 #pragma unroll
     for (int w = 1; w < kWavesP; ++w) kv_len = max(kv_len, red[1][w]);
     const int n_kt = (kv_len + kKT - 1) / kKT;
     const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
     const int lim = active ? tpos : -1;  // last key position this row may see
-    if (lim >= first_bad_key(a, bts, kv_len, lane)) aborted = true;
     // This workgroup's key tiles of the sequence: all of them, or its split.
     int t_lo = 0, t_hi = n_kt;
     if (a.split_tiles > 0) {
@@ -692,12 +711,45 @@ paged_prefill_kernel(PrefillArgs a) {
     // Double buffer: the next tile's direct loads are issued before this
     // tile's math; one wait + barrier per tile publishes it.
     if (t_lo < t_hi) {
+      // The first tile's block-table entry with a scalar load (its own
+      // counter: the fetch does not wait behind the Q loads in flight); the
+      // window for the later tiles is loaded by the next fetch.
+      int phys0 = -2;
+      if constexpr (!kPad) {
+        const int k0 = t_lo * kKT + 16 * wave;
+        const int bi = a.bs_shift >= 0 ? (k0 >> a.bs_shift) : k0 / a.block_size;
+        if (a.narrow && k0 + 16 <= kv_len && bi < a.max_blocks)
+          phys0 = scalar_load_i32(bts + bi);
+      }
       BlockWindow win;
-      window_load(a, bts, a.bs_shift >= 0 ? (t_lo * kKT) >> a.bs_shift
-                                          : (t_lo * kKT) / a.block_size, win);
-      tile_fetch<D, kPad>(a, bts, kbase, vbase, t_lo * kKT, kv_len, wave, lane, L, win, k0s, v0s);
+      if (phys0 >= -1) {
+        // Loaded by the first fetch that needs it.
+        win.base = -(1 << 30);
+        win.vals = -1;
+      } else {
+        window_load(a, bts, a.bs_shift >= 0 ? (t_lo * kKT) >> a.bs_shift
+                                            : (t_lo * kKT) / a.block_size, win);
+      }
+      tile_fetch<D, kPad>(a, bts, kbase, vbase, t_lo * kKT, kv_len, wave, lane, L, win, k0s, v0s,
+                          phys0);
+      // The abort check's table reads overlap the first tile's loads.
+      if (lim >= first_bad_key(a, bts, kv_len, lane)) aborted = true;
       wait_all();
       __builtin_amdgcn_s_barrier();
+      if constexpr (!Elem<T>::kSplitP) {
+        if (!q_ready) {
+          // fp16: Q prescaled by scale*log2(e), rounded once to fp16.
+#pragma unroll
+          for (int s2 = 0; s2 < C::NK; ++s2) {
+            f16x8 h = __builtin_bit_cast(f16x8, qb[s2]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              h[e] = static_cast<f16>(static_cast<float>(h[e]) * a.scale_log2);
+            qb[s2] = __builtin_bit_cast(u32x4, h);
+          }
+          q_ready = true;
+        }
+      }
       for (int kt = t_lo; kt < t_hi; kt += 2) {
         if (kt + 1 < t_hi)
           tile_fetch<D, kPad>(a, bts, kbase, vbase, (kt + 1) * kKT, kv_len, wave, lane, L, win, k1s,
@@ -715,6 +767,7 @@ paged_prefill_kernel(PrefillArgs a) {
         __builtin_amdgcn_s_barrier();
       }
     }
+    if (t_lo >= t_hi && lim >= first_bad_key(a, bts, kv_len, lane)) aborted = true;
     done = done || active;
   }
 
