@@ -58,11 +58,11 @@
 // read once per call, so its loads carry the nontemporal hint (MI355X
 // headline: 72 -> 79 % of HBM peak on one box; the hint on the earlier K lane
 // map, 16-byte pieces 64 bytes apart, had cost 8 points); the balanced
-// split hints V only (issue_tile).  Loads run one tile
-// ahead of the math in two buffers (the 4-wave fixed-partition kernel: two
-// tiles ahead in three rotating buffers), and the wave's block-table entries
-// sit in a VGPR (one per lane) read with readlane, so the steady-state loop
-// issues no scalar memory loads.
+// split hints V only (issue_tile).  Loads run one tile ahead of the math in
+// two buffers (the 4-wave fixed-partition kernel: two tiles ahead in three
+// rotating buffers), and the wave's block-table entries sit in a VGPR (one
+// per lane) read with readlane, so the steady-state loop issues no scalar
+// memory loads.
 #include "common.h"
 
 #include <atomic>
@@ -683,9 +683,9 @@ paged_decode_kernel(DecodeArgs a) {
   ro.whole = (n_parts == 1);
   ro.prow0 = (static_cast<int64_t>(seq) * a.num_q_heads + qh0) * a.max_parts + part;
   ro.prow_step = a.max_parts;
-  decode_range<D, T, NW, true, kPad, NW == 4 ? 2 : 1>(a, smem, seq, kvh, qh0, nh, L,
-                         a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro, false, part == 0,
-                         pre);
+  decode_range<D, T, NW, true, kPad, NW == 4 ? 2 : 1>(
+      a, smem, seq, kvh, qh0, nh, L, a.new_k != nullptr && Lorig == L, hc == 0, t0, t1, ro,
+      false, part == 0, pre);
 }
 
 // Balanced split: the tiles of all sequences (for one kv head) are laid end
