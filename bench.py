@@ -910,6 +910,11 @@ def main() -> int:
         },
         "device": torch.cuda.get_device_name(0),
     }
+    # A measured streaming bandwidth beside the 8 TB/s peak: a plain device
+    # copy (torch's copy_) moving the step's algorithmic bytes, half read and
+    # half written, timed after the record's own region.  The decode's stream
+    # is almost all reads, which HBM serves faster than a read/write mix.
+    res["streaming_copy"] = _vs_copy(kern_avg_ms, alg_bytes, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds)
     print(json.dumps(res))
