@@ -915,6 +915,19 @@ def main() -> int:
     # half written, timed after the record's own region.  The decode's stream
     # is almost all reads, which HBM serves faster than a read/write mix.
     res["streaming_copy"] = _vs_copy(kern_avg_ms, alg_bytes, args.steps, args.warmup)
+    # The measured ceiling of the decode's own stream: the same K and V rows
+    # read through the same block tables by a kernel that does nothing else
+    # with them (vaa_kv_stream_read), timed like the record's region.
+    sink = torch.empty((b.num_seqs, b.num_kv_heads), dtype=torch.int32, device=dev)
+    kv_bytes = int(b.seq_lens.sum().item()) * b.num_kv_heads * b.head_size * 2 * 2
+    t_rs = _timed(lambda: kernels.kv_stream_read(b.k_cache, b.v_cache, b.block_table,
+                                                 b.seq_lens, sink=sink),
+                  args.steps, args.warmup)
+    rs_gbs = kv_bytes / (t_rs * 1e-3) / 1e9
+    res["read_stream"] = {"kernel": "kv_stream_kernel<128>", "bytes": kv_bytes,
+                          "ms": round(t_rs, 5), "gb_s": round(rs_gbs, 1),
+                          "pct_hbm_peak": round(100 * rs_gbs / HBM_PEAK_GBS, 2),
+                          "decode_vs_read_stream": round(achieved / rs_gbs, 4)}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds)
     print(json.dumps(res))

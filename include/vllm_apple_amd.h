@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VAA_ABI_VERSION 4
+#define VAA_ABI_VERSION 5
 
 enum {
   VAA_OK = 0,
@@ -471,6 +471,27 @@ int vaa_topk_workspace_size(int num_tokens, int vocab_size, int k, size_t* works
 int vaa_topk_logits(const uint16_t* logits, int num_tokens, int vocab_size,
                     int64_t row_stride, int k, int32_t* indices, uint16_t* values,
                     int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Measurement aid
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Read-only stream of the K and V rows a paged decode step reads, the
+ * measured ceiling beside the decode's HBM roofline.  No counterpart in the
+ * reference.  Reads, through block_table, the rows of positions
+ * [0, seq_lens[s]) of every sequence s and kv head h with the decode's loads,
+ * and writes their checksum:
+ *   sink[s * num_kv_heads + h] = XOR of every 32-bit word of those K and V rows
+ * (rows whose table entry is negative, >= num_blocks or past
+ * max_blocks_per_seq are skipped; seq_len <= 0 gives 0).  Uses the cache
+ * fields of p (num_seqs, max_blocks_per_seq, head_size 32/64/96/128,
+ * block_size a multiple of 16, num_kv_heads, num_blocks, k/v strides); sink
+ * holds num_seqs * num_kv_heads uint32.
+ */
+int vaa_kv_stream_read(const vaa_attn_params* p, const uint16_t* key_cache,
+                       const uint16_t* value_cache, const int32_t* block_table,
+                       const int32_t* seq_lens, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

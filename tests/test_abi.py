@@ -77,7 +77,7 @@ def test_params_struct_layout_matches_header(tmp_path):
 
 
 def test_version_and_error_string_without_gpu(lib):
-    assert lib.vaa_abi_version() == 4
+    assert lib.vaa_abi_version() == 5
     from vllm_apple_amd import _lib
 
     assert isinstance(_lib.last_error(), str)

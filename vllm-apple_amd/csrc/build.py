@@ -32,6 +32,7 @@ SOURCES = [
     "qkv_epilogue.hip",
     "topk.hip",
     "gate_up_silu.hip",
+    "kv_stream.hip",
 ]
 
 ARCH = os.environ.get("VAA_OFFLOAD_ARCH", "gfx950")

@@ -35,7 +35,7 @@ VAA_PARTITION_BALANCED_SHARED = -2
 # Element types of caches, queries, new K/V and outputs (vaa_attn_params.dtype).
 VAA_DTYPE_F16 = 0
 VAA_DTYPE_BF16 = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class NativeLibraryError(RuntimeError):
@@ -112,6 +112,7 @@ SIGNATURES = {
     "vaa_topk_logits": (_I, [_P, _I, _I, _I64, _I, _P, _P, _I64, _P, ctypes.c_size_t, _P]),
     "vaa_qkv_epilogue": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _I,
                               _P]),
+    "vaa_kv_stream_read": (_I, [_PARAMS, _P, _P, _P, _P, _P, _P]),
 }
 
 _lock = threading.Lock()
@@ -138,12 +139,18 @@ def load() -> ctypes.CDLL:
             lib = ctypes.CDLL(str(_LIB_PATH), mode=ctypes.RTLD_GLOBAL)
         except OSError as e:
             raise NativeLibraryError(f"cannot load {_LIB_PATH}: {e}") from e
+        # The version first: a library built from other sources may lack
+        # symbols this module binds.
+        lib.vaa_abi_version.restype = _I
+        lib.vaa_abi_version.argtypes = []
+        if lib.vaa_abi_version() != ABI_VERSION:
+            raise NativeLibraryError(
+                f"ABI version mismatch: {_LIB_PATH} has {lib.vaa_abi_version()}, "
+                f"this package needs {ABI_VERSION} (rebuild the library)")
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.vaa_abi_version() != ABI_VERSION:
-            raise NativeLibraryError("ABI version mismatch")
         _lib = lib
         return lib
 

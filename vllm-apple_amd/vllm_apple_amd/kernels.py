@@ -855,6 +855,30 @@ def topk_logits(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = 
     return indices, values
 
 
+def kv_stream_read(key_cache: torch.Tensor, value_cache: torch.Tensor,
+                   block_table: torch.Tensor, seq_lens: torch.Tensor, *, layout: str = "kernel",
+                   sink: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Read-only stream of the K and V rows a paged decode of these tables
+    reads (vaa_kv_stream_read): the measured ceiling beside the decode's HBM
+    roofline.  Returns sink, int32 [num_seqs, num_kv_heads]: the XOR of every
+    32-bit word of the rows [0, seq_lens[s]) of sequence s and kv head h, read
+    through block_table (rows in an invalid table entry skipped)."""
+    _require_gpu(key_cache, value_cache, block_table, seq_lens, sink)
+    _check_tables(block_table, seq_lens)
+    num_seqs = seq_lens.numel()
+    p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
+                    num_query_heads=cache_strides(key_cache, layout).num_kv_heads, scale=1.0,
+                    num_seqs=num_seqs, max_blocks_per_seq=block_table.shape[1])
+    if sink is None:
+        sink = torch.empty((num_seqs, p.num_kv_heads), dtype=torch.int32, device=key_cache.device)
+    if sink.dtype != torch.int32 or not sink.is_contiguous() or sink.numel() < num_seqs * p.num_kv_heads:
+        raise ValueError("sink must be a contiguous int32 tensor of num_seqs * num_kv_heads entries")
+    _lib.call("vaa_kv_stream_read", ctypes.byref(p), key_cache.data_ptr(), value_cache.data_ptr(),
+              block_table.data_ptr(), seq_lens.data_ptr(), sink.data_ptr(),
+              _lib.stream_handle(stream))
+    return sink
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None,
              stream=None) -> torch.Tensor:
     """out = round16(silu(float(gate)) * float(up)); 1-D or row-strided 2-D views;
