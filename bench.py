@@ -393,6 +393,28 @@ def _decode_record(name: str, b, args, partition: int, note: str) -> dict:
             "tokens_per_s": round(b.num_seqs / (ms * 1e-3), 1)}
 
 
+def _read_stream(b, args, partition: int) -> dict:
+    """The K/V rows of a decode record read by vaa_kv_stream_read in the same
+    pieces (partition tokens per workgroup, 0: one per sequence), timed like
+    the record: the ceiling of that decomposition's stream."""
+    import torch
+
+    from vllm_apple_amd import kernels
+
+    parts = -(-b.max_seq_len // partition) if partition else 1
+    sink = torch.empty((b.num_seqs, parts, b.num_kv_heads), dtype=torch.int32,
+                       device=b.k_cache.device)
+    kv_bytes = int(b.seq_lens.sum().item()) * b.num_kv_heads * b.head_size * 2 * 2
+    t = _timed(lambda: kernels.kv_stream_read(b.k_cache, b.v_cache, b.block_table, b.seq_lens,
+                                              partition_size=partition,
+                                              max_seq_len=b.max_seq_len, sink=sink),
+               args.steps, args.warmup)
+    gbs = kv_bytes / (t * 1e-3) / 1e9
+    return {"kernel": "kv_stream_kernel<128>", "partition": partition or "none",
+            "bytes": kv_bytes, "ms": round(t, 5), "gb_s": round(gbs, 1),
+            "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+
+
 def wl_c1(args) -> dict:
     import torch
 
@@ -428,6 +450,7 @@ def wl_c4(args) -> dict:
     rauto = _decode_record("C4", b, args, 0, "partition chosen from lengths")
     r512["auto_partition"] = {k: rauto[k] for k in ("partition", "ms_per_step", "gb_s",
                                                    "pct_hbm_peak")}
+    r512["read_stream"] = _read_stream(b, args, 512)
     r512["scaled_key_rows"] = b.extra["scaled_rows"]
     if not args.no_cpu_baseline:
         # A quarter of the batch keeps the sample to a few seconds per step.
@@ -918,16 +941,9 @@ def main() -> int:
     # The measured ceiling of the decode's own stream: the same K and V rows
     # read through the same block tables by a kernel that does nothing else
     # with them (vaa_kv_stream_read), timed like the record's region.
-    sink = torch.empty((b.num_seqs, b.num_kv_heads), dtype=torch.int32, device=dev)
-    kv_bytes = int(b.seq_lens.sum().item()) * b.num_kv_heads * b.head_size * 2 * 2
-    t_rs = _timed(lambda: kernels.kv_stream_read(b.k_cache, b.v_cache, b.block_table,
-                                                 b.seq_lens, sink=sink),
-                  args.steps, args.warmup)
-    rs_gbs = kv_bytes / (t_rs * 1e-3) / 1e9
-    res["read_stream"] = {"kernel": "kv_stream_kernel<128>", "bytes": kv_bytes,
-                          "ms": round(t_rs, 5), "gb_s": round(rs_gbs, 1),
-                          "pct_hbm_peak": round(100 * rs_gbs / HBM_PEAK_GBS, 2),
-                          "decode_vs_read_stream": round(achieved / rs_gbs, 4)}
+    rs = _read_stream(b, args, 0)
+    rs["decode_vs_read_stream"] = round(achieved / rs["gb_s"], 4)
+    res["read_stream"] = rs
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_decode_step(b, args.cpu_seconds)
     print(json.dumps(res))

@@ -481,13 +481,17 @@ int vaa_topk_logits(const uint16_t* logits, int num_tokens, int vocab_size,
  * measured ceiling beside the decode's HBM roofline.  No counterpart in the
  * reference.  Reads, through block_table, the rows of positions
  * [0, seq_lens[s]) of every sequence s and kv head h with the decode's loads,
- * and writes their checksum:
- *   sink[s * num_kv_heads + h] = XOR of every 32-bit word of those K and V rows
+ * cut into pieces as the decode's fixed split-K partitions cut a context
+ * (p->partition_size P, a multiple of 16, with parts = ceil(max_seq_len / P)
+ * pieces per sequence; 0: one piece, parts = 1), one workgroup per piece, and
+ * writes their checksum:
+ *   sink[(s * parts + q) * num_kv_heads + h] = XOR of every 32-bit word of the
+ *       K and V rows of positions [q P, min((q + 1) P, seq_lens[s]))
  * (rows whose table entry is negative, >= num_blocks or past
- * max_blocks_per_seq are skipped; seq_len <= 0 gives 0).  Uses the cache
- * fields of p (num_seqs, max_blocks_per_seq, head_size 32/64/96/128,
- * block_size a multiple of 16, num_kv_heads, num_blocks, k/v strides); sink
- * holds num_seqs * num_kv_heads uint32.
+ * max_blocks_per_seq are skipped; an empty piece gives 0).  Uses the cache
+ * fields of p (num_seqs, max_seq_len, max_blocks_per_seq, head_size
+ * 32/64/96/128, block_size a multiple of 16, num_kv_heads, num_blocks, k/v
+ * strides, partition_size); sink holds num_seqs * parts * num_kv_heads uint32.
  */
 int vaa_kv_stream_read(const vaa_attn_params* p, const uint16_t* key_cache,
                        const uint16_t* value_cache, const int32_t* block_table,

@@ -11,37 +11,39 @@ from helpers import host
 pytestmark = pytest.mark.gpu
 
 
-def _xor_rows(k, v, bt, lens, layout):
-    """Host checksum: XOR of every 32-bit word of the K and V rows [0, L) of
-    each (sequence, kv head), rows in invalid table entries skipped."""
+def _xor_rows(k, v, bt, lens, layout, piece=0):
+    """Host checksum: XOR of every 32-bit word of the K and V rows of each
+    (sequence, piece, kv head), pieces of `piece` tokens (0: the whole
+    context), rows in invalid table entries skipped."""
     nb = k.shape[0]
     bs = k.shape[2] if layout == "kernel" else k.shape[1]
     kv = k.shape[1] if layout == "kernel" else k.shape[2]
-    out = np.zeros((len(lens), kv), dtype=np.uint32)
+    top = max(max(lens), 1)
+    parts = -(-top // piece) if piece else 1
+    out = np.zeros((len(lens), parts, kv), dtype=np.uint32)
     for s, L in enumerate(lens):
-        for h in range(kv):
-            acc = np.uint32(0)
-            for pos in range(max(L, 0)):
-                bi = pos // bs
-                if bi >= bt.shape[1]:
-                    break
-                phys = int(bt[s, bi])
-                if phys < 0 or phys >= nb:
-                    continue
-                o = pos % bs
+        for pos in range(max(L, 0)):
+            bi = pos // bs
+            if bi >= bt.shape[1]:
+                break
+            phys = int(bt[s, bi])
+            if phys < 0 or phys >= nb:
+                continue
+            o, q = pos % bs, (pos // piece if piece else 0)
+            for h in range(kv):
                 for c in (k, v):
                     row = c[phys, h, o] if layout == "kernel" else c[phys, o, h]
-                    acc ^= np.bitwise_xor.reduce(np.ascontiguousarray(row).view(np.uint32))
-            out[s, h] = acc
+                    out[s, q, h] ^= np.bitwise_xor.reduce(np.ascontiguousarray(row).view(np.uint32))
     return out
 
 
 @pytest.mark.parametrize("layout", ["kernel", "vllm"])
 @pytest.mark.parametrize("kv,d,bs", [(8, 128, 16), (2, 64, 32), (4, 96, 16), (1, 32, 48)])
-def test_kv_stream_checksum(gpu, layout, kv, d, bs):
+@pytest.mark.parametrize("piece", [0, 32, 48])
+def test_kv_stream_checksum(gpu, layout, kv, d, bs, piece):
     from vllm_apple_amd import kernels
 
-    print(f"[case] kv_stream layout={layout} kv={kv} d={d} bs={bs}", flush=True)
+    print(f"[case] kv_stream layout={layout} kv={kv} d={d} bs={bs} piece={piece}", flush=True)
     g = torch.Generator().manual_seed(11)
     nb, max_blocks = 128, 12
     shape = (nb, kv, bs, d) if layout == "kernel" else (nb, bs, kv, d)
@@ -53,8 +55,9 @@ def test_kv_stream_checksum(gpu, layout, kv, d, bs):
     bt[6, 2] = -1          # a missing block inside a context
     bt[8, 1] = nb + 5      # past the cache: skipped
     seq_lens = torch.tensor(lens, dtype=torch.int32)
-    ref = _xor_rows(host(kc), host(vc), host(bt), lens, layout)
-    sink = kernels.kv_stream_read(kc.cuda(), vc.cuda(), bt.cuda(), seq_lens.cuda(), layout=layout)
+    ref = _xor_rows(host(kc), host(vc), host(bt), lens, layout, piece)
+    sink = kernels.kv_stream_read(kc.cuda(), vc.cuda(), bt.cuda(), seq_lens.cuda(), layout=layout,
+                                  partition_size=piece, max_seq_len=max(lens))
     torch.cuda.synchronize()
     got = host(sink).view(np.uint32)
     assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
@@ -72,7 +75,7 @@ def test_kv_stream_headline_shape(gpu):
     L = 8192
     nblk = L // 16
     rows = b.block_table[:, :nblk].long()                     # [B, nblk]
-    got = sink.cpu().view(torch.int32)
+    got = sink[:, 0].cpu()
     for c in (b.k_cache, b.v_cache):
         x = c[rows]                                           # [B, nblk, KV, 16, D]
         x = x.permute(0, 2, 1, 3, 4).reshape(x.shape[0], x.shape[2], -1)

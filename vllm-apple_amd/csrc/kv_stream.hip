@@ -5,23 +5,26 @@
 // with the same loads (16 bytes per lane, nontemporal) and does nothing else
 // with them but fold them into a checksum.
 //
-//   sink[s * num_kv_heads + h] = XOR of every 32-bit word of the K and V rows
-//                                of positions [0, seq_lens[s]) of sequence s,
-//                                kv head h
+//   sink[(s * parts + q) * num_kv_heads + h] = XOR of every 32-bit word of
+//       the K and V rows of positions [q * P, min((q + 1) * P, seq_lens[s]))
+//       of sequence s, kv head h
 //
-// Rows whose block-table entry is negative or past num_blocks, or lies past
-// max_blocks_per_seq, are skipped; a sequence with seq_len <= 0 gives 0.
-// One 8-wave workgroup per (sequence, kv head), as the decode runs one
-// sequence per workgroup at the headline shape; wave w takes the 16-token
-// tiles w, w + 8, ... and keeps the loads of the next tile in flight while it
-// folds the current one.
+// with P = partition_size (parts = ceil(max_seq_len / P)) as the decode's
+// fixed split-K partitions cut a context, or P = infinity (parts = 1) when
+// partition_size is 0.  Rows whose block-table entry is negative or past
+// num_blocks, or lies past max_blocks_per_seq, are skipped; an empty piece
+// gives 0.  One workgroup per (kv head, piece, sequence), kv head fastest, as
+// the decode's grid: 8 waves, or 4 for pieces of up to 1024 tokens (the
+// decode's short partitions); wave w takes the piece's 16-token tiles w,
+// w + NW, ... and keeps the loads of the next tile in flight while it folds
+// the current one.
 #include "common.h"
 
 namespace vaa {
 namespace {
 
-constexpr int kStreamWaves = 8;
 constexpr int kStreamTile = 16;  // tokens per tile, inside one block
+constexpr int kShortPiece = 1024;  // pieces up to this many tokens run 4 waves
 
 struct StreamArgs {
   const char* kc;
@@ -30,6 +33,7 @@ struct StreamArgs {
   const int32_t* seq_lens;
   uint32_t* sink;
   int max_blocks, block_size, num_kv_heads;
+  int piece_tiles, parts;  // 16-token tiles per piece, pieces per sequence
   int64_t num_blocks;
   int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;  // byte strides
 };
@@ -77,26 +81,33 @@ __device__ __forceinline__ uint32_t stream_fold(const STile<D>& t) {
   return x;
 }
 
-template <int D>
-__global__ void __launch_bounds__(kStreamWaves * kWave) kv_stream_kernel(StreamArgs a) {
-  __shared__ uint32_t red[kStreamWaves];
-  const int s = blockIdx.x, h = blockIdx.y;
+template <int D, int NW>
+__global__ void __launch_bounds__(NW * kWave) kv_stream_kernel(StreamArgs a) {
+  __shared__ uint32_t red[NW];
+  const int h = blockIdx.x, q = blockIdx.y, s = blockIdx.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int len = a.seq_lens[s];
   const int ntiles = len > 0 ? (len + kStreamTile - 1) / kStreamTile : 0;
+  const int t_lo = q * a.piece_tiles;
+  const int t_hi = min(ntiles, t_lo + a.piece_tiles);
   const int32_t* bts = a.bt + static_cast<int64_t>(s) * a.max_blocks;
   const char* kh = a.kc + h * a.k_sh;
   const char* vh = a.vc + h * a.v_sh;
   uint32_t x = 0;
-  STile<D> t0, t1;
-  int j = wave;
-  stream_issue<D>(a, bts, len, kh, vh, j, lane, t0);
-  for (; j < ntiles; j += 2 * kStreamWaves) {
-    stream_issue<D>(a, bts, len, kh, vh, j + kStreamWaves, lane, t1);
-    x ^= stream_fold<D>(t0);
-    stream_issue<D>(a, bts, len, kh, vh, j + 2 * kStreamWaves, lane, t0);
-    x ^= stream_fold<D>(t1);
+  if (t_lo < t_hi) {
+    // Tiles past t_hi load nothing: stream_issue zeroes rows past the
+    // piece's last key.
+    const int lim = min(len, t_hi * kStreamTile);
+    STile<D> t0, t1;
+    int j = t_lo + wave;
+    stream_issue<D>(a, bts, lim, kh, vh, j, lane, t0);
+    for (; j < t_hi; j += 2 * NW) {
+      stream_issue<D>(a, bts, lim, kh, vh, j + NW, lane, t1);
+      x ^= stream_fold<D>(t0);
+      stream_issue<D>(a, bts, lim, kh, vh, j + 2 * NW, lane, t0);
+      x ^= stream_fold<D>(t1);
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o, kWave);
@@ -105,9 +116,17 @@ __global__ void __launch_bounds__(kStreamWaves * kWave) kv_stream_kernel(StreamA
   if (threadIdx.x == 0) {
     uint32_t r = 0;
 #pragma unroll
-    for (int w = 0; w < kStreamWaves; ++w) r ^= red[w];
-    a.sink[static_cast<int64_t>(s) * a.num_kv_heads + h] = r;
+    for (int w = 0; w < NW; ++w) r ^= red[w];
+    a.sink[(static_cast<int64_t>(s) * a.parts + q) * a.num_kv_heads + h] = r;
   }
+}
+
+template <int D>
+void launch_stream(const StreamArgs& a, dim3 grid, bool short_pieces, hipStream_t s) {
+  if (short_pieces)
+    hipLaunchKernelGGL((kv_stream_kernel<D, 4>), grid, dim3(4 * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((kv_stream_kernel<D, 8>), grid, dim3(8 * kWave), 0, s, a);
 }
 
 }  // namespace
@@ -124,12 +143,15 @@ extern "C" int vaa_kv_stream_read(const vaa_attn_params* p, const uint16_t* key_
   if (D != 32 && D != 64 && D != 96 && D != 128)
     return fail(VAA_ERR_UNSUPPORTED, "%s: head_size=%d (32, 64, 96 or 128)", what, D);
   if (p->num_seqs < 0 || p->num_kv_heads <= 0 || p->block_size <= 0 ||
-      p->block_size % kStreamTile != 0 || p->max_blocks_per_seq <= 0 || p->num_blocks <= 0)
+      p->block_size % kStreamTile != 0 || p->max_blocks_per_seq <= 0 || p->num_blocks <= 0 ||
+      p->partition_size < 0 || p->partition_size % kStreamTile != 0 ||
+      (p->partition_size > 0 && p->max_seq_len <= 0))
     return fail(VAA_ERR_INVALID_ARG,
                 "%s: num_seqs=%d num_kv_heads=%d block_size=%d (a multiple of 16) "
-                "max_blocks_per_seq=%d num_blocks=%lld",
+                "max_blocks_per_seq=%d num_blocks=%lld partition_size=%d (0 or a multiple of "
+                "16, with max_seq_len > 0) max_seq_len=%d",
                 what, p->num_seqs, p->num_kv_heads, p->block_size, p->max_blocks_per_seq,
-                (long long)p->num_blocks);
+                (long long)p->num_blocks, p->partition_size, p->max_seq_len);
   if (p->num_seqs == 0) return VAA_OK;
   if (!key_cache || !value_cache || !block_table || !seq_lens || !sink)
     return fail(VAA_ERR_INVALID_ARG, "%s: null pointer", what);
@@ -139,8 +161,11 @@ extern "C" int vaa_kv_stream_read(const vaa_attn_params* p, const uint16_t* key_
     return fail(VAA_ERR_INVALID_ARG,
                 "%s: caches must be 16-byte aligned with strides in multiples of 8 elements",
                 what);
-  if (p->num_kv_heads > 65535)
-    return fail(VAA_ERR_UNSUPPORTED, "%s: num_kv_heads=%d", what, p->num_kv_heads);
+  const int P = p->partition_size;
+  const int parts = P > 0 ? (p->max_seq_len + P - 1) / P : 1;
+  if (p->num_seqs > 65535 || parts > 65535)
+    return fail(VAA_ERR_UNSUPPORTED, "%s: num_seqs=%d pieces per sequence=%d (at most 65535)",
+                what, p->num_seqs, parts);
   StreamArgs a;
   a.kc = reinterpret_cast<const char*>(key_cache);
   a.vc = reinterpret_cast<const char*>(value_cache);
@@ -150,6 +175,8 @@ extern "C" int vaa_kv_stream_read(const vaa_attn_params* p, const uint16_t* key_
   a.max_blocks = p->max_blocks_per_seq;
   a.block_size = p->block_size;
   a.num_kv_heads = p->num_kv_heads;
+  a.piece_tiles = P > 0 ? P / kStreamTile : (1 << 30) / kStreamTile;
+  a.parts = parts;
   a.num_blocks = p->num_blocks;
   a.k_sb = 2 * p->k_stride_block;
   a.k_sh = 2 * p->k_stride_head;
@@ -157,13 +184,14 @@ extern "C" int vaa_kv_stream_read(const vaa_attn_params* p, const uint16_t* key_
   a.v_sb = 2 * p->v_stride_block;
   a.v_sh = 2 * p->v_stride_head;
   a.v_st = 2 * p->v_stride_token;
-  const dim3 grid(p->num_seqs, p->num_kv_heads);
+  const dim3 grid(p->num_kv_heads, parts, p->num_seqs);
+  const bool short_pieces = P > 0 && P <= kShortPiece;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (D) {
-    case 32: hipLaunchKernelGGL(kv_stream_kernel<32>, grid, dim3(kStreamWaves * kWave), 0, s, a); break;
-    case 64: hipLaunchKernelGGL(kv_stream_kernel<64>, grid, dim3(kStreamWaves * kWave), 0, s, a); break;
-    case 96: hipLaunchKernelGGL(kv_stream_kernel<96>, grid, dim3(kStreamWaves * kWave), 0, s, a); break;
-    default: hipLaunchKernelGGL(kv_stream_kernel<128>, grid, dim3(kStreamWaves * kWave), 0, s, a); break;
+    case 32: launch_stream<32>(a, grid, short_pieces, s); break;
+    case 64: launch_stream<64>(a, grid, short_pieces, s); break;
+    case 96: launch_stream<96>(a, grid, short_pieces, s); break;
+    default: launch_stream<128>(a, grid, short_pieces, s); break;
   }
   return check_launch(what);
 }

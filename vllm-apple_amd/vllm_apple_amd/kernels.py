@@ -857,22 +857,33 @@ def topk_logits(logits: torch.Tensor, k: int, *, indices: torch.Tensor | None = 
 
 def kv_stream_read(key_cache: torch.Tensor, value_cache: torch.Tensor,
                    block_table: torch.Tensor, seq_lens: torch.Tensor, *, layout: str = "kernel",
+                   partition_size: int = 0, max_seq_len: int = 0,
                    sink: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """Read-only stream of the K and V rows a paged decode of these tables
     reads (vaa_kv_stream_read): the measured ceiling beside the decode's HBM
-    roofline.  Returns sink, int32 [num_seqs, num_kv_heads]: the XOR of every
-    32-bit word of the rows [0, seq_lens[s]) of sequence s and kv head h, read
+    roofline.  With partition_size P > 0 (a multiple of 16; max_seq_len
+    bounds seq_lens) each sequence is read in pieces of P tokens, one
+    workgroup per piece, as the decode's fixed partitions cut it.  Returns
+    sink, int32 [num_seqs, parts, num_kv_heads] (parts = ceil(max_seq_len / P),
+    or 1): the XOR of every 32-bit word of the piece's K and V rows, read
     through block_table (rows in an invalid table entry skipped)."""
     _require_gpu(key_cache, value_cache, block_table, seq_lens, sink)
     _check_tables(block_table, seq_lens)
     num_seqs = seq_lens.numel()
     p = make_params(key_cache=key_cache, value_cache=value_cache, layout=layout,
                     num_query_heads=cache_strides(key_cache, layout).num_kv_heads, scale=1.0,
-                    num_seqs=num_seqs, max_blocks_per_seq=block_table.shape[1])
+                    num_seqs=num_seqs, max_seq_len=max_seq_len,
+                    max_blocks_per_seq=block_table.shape[1], partition_size=partition_size)
+    parts = -(-max_seq_len // partition_size) if partition_size > 0 else 1
+    if partition_size > 0 and max_seq_len <= 0:
+        raise ValueError("partition_size needs max_seq_len > 0")
     if sink is None:
-        sink = torch.empty((num_seqs, p.num_kv_heads), dtype=torch.int32, device=key_cache.device)
-    if sink.dtype != torch.int32 or not sink.is_contiguous() or sink.numel() < num_seqs * p.num_kv_heads:
-        raise ValueError("sink must be a contiguous int32 tensor of num_seqs * num_kv_heads entries")
+        sink = torch.empty((num_seqs, parts, p.num_kv_heads), dtype=torch.int32,
+                           device=key_cache.device)
+    if sink.dtype != torch.int32 or not sink.is_contiguous() \
+            or sink.numel() < num_seqs * parts * p.num_kv_heads:
+        raise ValueError("sink must be a contiguous int32 tensor of "
+                         "num_seqs * parts * num_kv_heads entries")
     _lib.call("vaa_kv_stream_read", ctypes.byref(p), key_cache.data_ptr(), value_cache.data_ptr(),
               block_table.data_ptr(), seq_lens.data_ptr(), sink.data_ptr(),
               _lib.stream_handle(stream))
