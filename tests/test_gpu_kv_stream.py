@@ -88,3 +88,25 @@ def test_kv_stream_headline_shape(gpu):
         else:
             ref = torch.bitwise_xor(ref, w[..., 0])
     assert torch.equal(got, ref.cpu())
+
+
+def test_kv_stream_rejects_bad_arguments(gpu):
+    """Unsupported head sizes and piece sizes fail before any launch, with the
+    library's status mapped to the Python exception."""
+    from vllm_apple_amd import kernels
+
+    print("[case] kv_stream errors", flush=True)
+    dev = torch.device("cuda:0")
+    bt = torch.zeros((2, 4), dtype=torch.int32, device=dev)
+    lens = torch.tensor([16, 40], dtype=torch.int32, device=dev)
+    k80 = torch.zeros((8, 2, 16, 80), dtype=torch.float16, device=dev)
+    with pytest.raises(NotImplementedError, match="head_size=80"):
+        kernels.kv_stream_read(k80, k80.clone(), bt, lens)
+    k = torch.zeros((8, 2, 16, 64), dtype=torch.float16, device=dev)
+    with pytest.raises(ValueError, match="partition_size=24"):
+        kernels.kv_stream_read(k, k.clone(), bt, lens, partition_size=24, max_seq_len=40)
+    with pytest.raises(ValueError, match="max_seq_len"):
+        kernels.kv_stream_read(k, k.clone(), bt, lens, partition_size=32)
+    with pytest.raises(ValueError, match="sink"):
+        kernels.kv_stream_read(k, k.clone(), bt, lens,
+                               sink=torch.zeros(3, dtype=torch.int32, device=dev))
